@@ -1,0 +1,291 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused SDPA forward on one MI355X (the BASELINE.json metric).
+
+Headline workload: C64 = B2 H8 N2048 D64, fp16 in / fp32 accumulate,
+non-causal, through the stage-5 kernel (``fa_s5_tuned``, what ``torch.ops.fused_attn.forward``
+dispatches to for fp16). A *step* is one forward over one batch of synthetic inputs already
+resident in HBM. The kernel is launched through the C-ABI (``fa_forward`` of libfa_hip.so) on a
+dedicated HIP stream, and HIP events recorded on that same stream bracket the K timed steps.
+
+Printed: ONE JSON line with the contract fields, plus
+* ``roofline``: MFMA-bound; achieved = 4*B*H*N^2*D FLOPs per launch / average launch duration;
+  peak = 2.5 PFLOP/s dense fp16; ``traffic`` = HBM bytes per launch from the committed
+  ``rocprofv3 --pmc`` summary (profiles/), or null when none is committed for the workload;
+* ``cpu_baseline``: the reference's own fp64 CPU oracle (oracle/_ref, ``fa::ref::attention_rows``,
+  kind "reference"; the C restatement, kind "port", when _ref is absent) timed on the host cores over
+  a bounded sample of the same workload;
+* ``configs``: the other BASELINE configurations measured the same way (C128, C128 causal, LONG,
+  GPT attention shape), each with ms and TFLOP/s;
+* ``protocol``: the reference's timing protocol (ref:docs/BENCHMARK_PROTOCOL.md rules 1-2) on the
+  headline workload: 1 GiB flush before every launch, one event pair per launch, median/p10/p90.
+
+Before any timing, the output is checked against the fp64 oracle on selected rows (the reference
+refuses to write a row otherwise, ref:docs/BENCHMARK_PROTOCOL.md rule 3).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "fused-attention-cuda_amd"))
+
+METRIC = "fwd ms + TFLOP/s, B2 H8 N2048 D64/D128 fp16; % of MFMA fp16 peak"
+PEAK_TFLOPS = {"fp16": 2500.0, "bf16": 2500.0, "fp32": 157.3}  # MI355X dense MFMA
+# (name, B, H, N, D, dtype, causal, input std): BASELINE.json configs[1..4] (attention shapes).
+WORKLOADS = {
+    "C64": (2, 8, 2048, 64, "fp16", False, 1.0),
+    "C128": (2, 8, 2048, 128, "fp16", False, 1.0),
+    "C128_causal": (2, 8, 2048, 128, "fp16", True, 1.0),
+    "LONG": (1, 16, 8192, 128, "bf16", True, 0.5),
+    "GPT_attn": (8, 12, 1024, 64, "fp16", True, 1.0),
+}
+
+
+def flops(b, h, n, d, causal) -> float:
+    """4*B*H*N^2*D, halved for causal (ref:docs/BENCHMARK_PROTOCOL.md rule 5)."""
+    f = 4.0 * b * h * n * n * d
+    return f / 2 if causal else f
+
+
+def hbm_bytes(b, h, n, d, esize) -> int:
+    """Algorithmic bytes: Q, K, V read + O written + LSE (ref:bench/bench_main.cu:570-580)."""
+    return 4 * b * h * n * d * esize + 4 * b * h * n
+
+
+def traffic_from_profiles(workload: str):
+    """HBM bytes per launch of the headline kernel, from the committed PMC summary, or None."""
+    f = ROOT / "profiles" / f"fa_s5_tuned_{workload}_traffic.md"
+    if not f.exists():
+        return None
+    m = re.search(r"hbm_bytes_per_launch:\s*([0-9.eE+]+)", f.read_text())
+    return float(m.group(1)) if m else None
+
+
+def make_inputs(torch, b, h, n, d, dtype, std, seed):
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    return tuple((torch.randn(b, h, n, d, generator=gen, device="cuda") * std).to(dtype)
+                 for _ in range(3))
+
+
+def gate(torch, capi, q, k, v, o, lse, causal, scale, stage, stream):
+    """Correctness gate before timing: selected rows of two heads vs the fp64 oracle."""
+    from oracle.oracle import math_reference_rows
+
+    rc = capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream)
+    if rc != 0:
+        raise RuntimeError(f"fa_forward failed: {capi.error_string(rc)}")
+    stream.synchronize()
+    b, h, n, d = q.shape
+    import numpy as np
+
+    rows = np.unique(np.r_[0:32, n - 32:n])
+    worst_o = worst_l = 0.0
+    for bi, hi in ((0, 0), (b - 1, h - 1)):
+        o64, l64 = math_reference_rows(q, k, v, bi, hi, rows, is_causal=causal, scale=scale)
+        eo = np.abs(o[bi, hi, rows].double().cpu().numpy() - o64)
+        if (eo > 2e-3 + 2e-3 * np.abs(o64)).any():
+            raise RuntimeError(f"correctness gate failed: max|O err| {eo.max():.3e}")
+        el = float(np.abs(lse[bi, hi, rows].double().cpu().numpy() - l64).max())
+        if el > 1e-3:
+            raise RuntimeError(f"correctness gate failed: max|LSE err| {el:.3e}")
+        worst_o, worst_l = max(worst_o, float(eo.max())), max(worst_l, el)
+    return worst_o, worst_l
+
+
+def time_steps(torch, capi, args_list, causal, scale, stage, stream, steps, warmup):
+    """Warmup, then K launches bracketed by events on the launch stream; average ms per launch.
+    args_list rotates over input sets (q, k, v, o, lse)."""
+    for i in range(warmup):
+        q, k, v, o, lse = args_list[i % len(args_list)]
+        capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream)
+    stream.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        q, k, v, o, lse = args_list[i % len(args_list)]
+        rc = capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream)
+        if rc != 0:
+            raise RuntimeError(f"fa_forward failed: {capi.error_string(rc)}")
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def protocol_timing(torch, capi, args_list, causal, scale, stage, stream, iters=100):
+    """Reference protocol: 1 GiB flush before every launch, one event pair per launch, median."""
+    flush = torch.empty(1 << 28, dtype=torch.int32, device="cuda")  # 1 GiB
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(iters)]
+    with torch.cuda.stream(stream):
+        for i in range(iters):
+            flush.zero_()
+            q, k, v, o, lse = args_list[i % len(args_list)]
+            evs[i][0].record(stream)
+            capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream)
+            evs[i][1].record(stream)
+    stream.synchronize()
+    ms = sorted(a.elapsed_time(b) for a, b in evs)
+    pct = lambda p: ms[min(len(ms) - 1, int(round(p / 100 * (len(ms) - 1))))]  # noqa: E731
+    del flush
+    return {"ms_median": pct(50), "ms_p10": pct(10), "ms_p90": pct(90), "iters": iters,
+            "flush_bytes": 1 << 30}
+
+
+def cpu_baseline(q, k, v, causal, scale, gpu_o, budget_s: float):
+    """The reference's CPU oracle on the host cores over a bounded sample of heads."""
+    import numpy as np
+
+    from oracle.oracle import COracle, RefOracle, to_f64
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    b, h, n, d = q.shape
+    q64, k64, v64 = to_f64(q), to_f64(k), to_f64(v)
+    if RefOracle.available():
+        ref, kind = RefOracle(), "reference"
+
+        def run(h0, nh):
+            return ref.attention_heads(q64, k64, v64, h0, nh, is_causal=causal, scale=scale,
+                                       threads=threads)
+    else:
+        cor, kind = COracle(), "port"
+
+        def run(h0, nh):
+            bi, hi = divmod(h0, h)
+            o1, l1 = cor.attention_rows(q64, k64, v64, bi, hi, 0, n, is_causal=causal,
+                                        scale=scale)
+            return o1[None], l1[None]
+    # Probe one head on one thread's worth of work, then size the sample to the budget.
+    t0 = time.perf_counter()
+    o_first, _ = run(0, 1)
+    t_head = time.perf_counter() - t0
+    total_heads = b * h
+    nheads = int(max(1, min(total_heads, (budget_s / max(t_head, 1e-6)) * threads)))
+    if kind == "port":
+        nheads = 1
+    t0 = time.perf_counter()
+    o_s, _ = run(0, nheads)
+    wall = time.perf_counter() - t0
+    # The CPU path computed the same function: compare its first head with the GPU's.
+    diff = float(np.abs(o_s[0] - gpu_o[0, 0].double().cpu().numpy()).max())
+    f = flops(1, nheads, n, d, causal)
+    return {"value": f / wall / 1e12, "unit": "TFLOP/s", "cores": threads if kind == "reference"
+            else 1, "kind": kind,
+            "sample": f"{nheads} of {total_heads} heads of the workload (all {n} rows each), "
+                      f"fp64, {wall:.2f} s wall; full-workload estimate "
+                      f"{wall * total_heads / nheads * 1e3:.0f} ms; max|O_cpu - O_gpu| on head 0 "
+                      f"{diff:.2e}",
+            "ms_full_workload_est": wall * total_heads / nheads * 1e3}
+
+
+def bench_workload(torch, capi, name, stage, steps, warmup, seed=0, gate_it=True):
+    b, h, n, d, dt, causal, std = WORKLOADS[name]
+    dtype = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[dt]
+    scale = 1.0 / math.sqrt(d)
+    stream = torch.cuda.Stream()
+    sets = []
+    with torch.cuda.stream(stream):
+        for s in range(4):  # four rotating input sets (ref:bench/bench_main.cu:717-725)
+            q, k, v = make_inputs(torch, b, h, n, d, dtype, std, seed + s)
+            o = torch.empty_like(q)
+            lse = torch.empty(b, h, n, dtype=torch.float32, device="cuda")
+            sets.append((q, k, v, o, lse))
+    stream.synchronize()
+    err = gate(torch, capi, *sets[0], causal, scale, stage, stream) if gate_it else (None, None)
+    ms = time_steps(torch, capi, sets, causal, scale, stage, stream, steps, warmup)
+    f = flops(b, h, n, d, causal)
+    tf = f / (ms * 1e-3) / 1e12
+    res = {"B": b, "H": h, "N": n, "D": d, "dtype": dt, "causal": causal, "stage": stage,
+           "ms": ms, "tflops": tf, "pct_peak": 100.0 * tf / PEAK_TFLOPS[dt], "flops": f,
+           "gate_max_err_o": err[0], "gate_max_err_lse": err[1]}
+    return res, sets, stream, causal, scale
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="C64", choices=sorted(WORKLOADS))
+    ap.add_argument("--stage", type=int, default=5, choices=(3, 4, 5))
+    ap.add_argument("--only", action="store_true",
+                    help="headline workload only: no other configs, no protocol, no CPU baseline "
+                         "(for profiler runs)")
+    ap.add_argument("--cpu-budget", type=float, default=12.0,
+                    help="target seconds of CPU baseline work (wall ~ this / threads)")
+    a = ap.parse_args(argv)
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU; multi-GPU runs are out of scope "
+              "(see the sharding note in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from fused_attn import capi
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 2
+    capi.load()
+    head, sets, stream, causal, scale = bench_workload(torch, capi, a.workload, a.stage, a.steps,
+                                                       a.warmup)
+    b, h, n, d, dt = head["B"], head["H"], head["N"], head["D"], head["dtype"]
+    achieved = head["tflops"]
+    esize = 2 if dt in ("fp16", "bf16") else 4
+    line = {
+        "metric": METRIC,
+        "value": round(achieved, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(head["ms"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dt,
+        "data": "synthetic (seeded N(0,1) on device, 4 rotating input sets)",
+        "config": {"workload": f"{a.workload}: B{b} H{h} N{n} D{d} {dt} "
+                               f"{'causal' if causal else 'non-causal'}, stage {a.stage} "
+                               f"(fa_s5_tuned)" if a.stage == 5 else
+                               f"{a.workload}: B{b} H{h} N{n} D{d} {dt} stage {a.stage}",
+                   "B": b, "H": h, "N": n, "D": d, "causal": causal, "stage": a.stage},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
+                     "peak": PEAK_TFLOPS[dt], "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_TFLOPS[dt], 5),
+                     "traffic": traffic_from_profiles(a.workload),
+                     "algorithmic_bytes": hbm_bytes(b, h, n, d, esize),
+                     "flops_per_launch": head["flops"]},
+        "pct_of_peak": round(head["pct_peak"], 3),
+        "gate": {"max_err_o": head["gate_max_err_o"], "max_err_lse": head["gate_max_err_lse"]},
+    }
+    if not a.only:
+        line["protocol"] = protocol_timing(torch, capi, sets, causal, scale, a.stage, stream)
+        q, k, v, o, lse = sets[0]
+        line["cpu_baseline"] = cpu_baseline(q, k, v, causal, scale, o, a.cpu_budget)
+        del sets
+        others = {}
+        for name in WORKLOADS:
+            if name == a.workload:
+                continue
+            res, s2, _, _, _ = bench_workload(torch, capi, name, 5, max(20, a.steps // 4),
+                                              a.warmup)
+            del s2
+            others[name] = {kk: (round(vv, 6) if isinstance(vv, float) else vv)
+                            for kk, vv in res.items()}
+        line["configs"] = others
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,598 @@
+// attn_kernel.h -- the gfx950 fused SDPA forward kernel template (device code + launch helper).
+//
+// Included by attn_f16.hip, attn_bf16.hip and attn_f32.hip, which instantiate it. One template
+// serves three stage slots of the reference ladder:
+//   fa_s5_tuned<T>   (stage 5)  fp16/bf16 operands on v_mfma_f32_32x32x16_{f16,bf16}, K/V tiles
+//                               double-buffered in LDS with the next tile's global loads issued
+//                               into registers before the current tile's math (the role of the
+//                               reference's PREFETCH knob, ref:src/stage5_tuned.cu:29-47);
+//   fa_s4_mfma<T>    (stage 4)  the same kernel with synchronous staging (one LDS buffer, load ->
+//                               barrier -> math -> barrier), the reference's S4 = S5 with PREFETCH
+//                               off (ref:src/stage5_tuned.cu:1-8);
+//   fa_s3_fused<T>   (stage 3)  the fp32-compute correctness rung: operands are held in LDS as fp32
+//                               and multiplied on v_mfma_f32_32x32x2_f32, so no operand is rounded
+//                               below fp32 (fp32 or fp16 I/O, ref:src/stage3_fused.cu:142-160).
+//
+// Algorithm (FlashAttention-2 loop order, the reference's recurrence ref:include/fa/softmax_math.cuh):
+// a workgroup owns BR = 32*WAVES query rows of one (b, h); each wave owns 32 rows for the whole
+// kernel; K/V tiles of BC keys stream through LDS; per tile a wave computes S^T = K Q^T on MFMA,
+// masks (causal diagonal block only), updates the running max m (raw score units), rescales
+// (alpha = exp2((m_old - m_new) c), c = scale*log2 e), exponentiates p = exp2(s c - m c), sums l,
+// and accumulates O^T += V^T P^T on MFMA. Epilogue: O = acc / l, lse = m*scale + ln l. Causal key
+// tiles beyond the workgroup's last row are never loaded; per wave, key blocks beyond the wave's
+// last row are skipped and only the diagonal 32x32 block is masked.
+//
+// WHY S^T = K Q^T (not S = Q K^T): the 32x32 MFMA accumulator gives lane l the column n = l % 32
+// and 16 rows m = 8(r/4) + 4(l/32) + r%4 (r = register). With M = keys and N = query rows, every
+// lane owns ONE query row and 16 of its keys, so (a) the row max/sum needs a single cross-lane
+// step (lane l with l ^ 32), (b) alpha is one scalar per lane, and (c) the probabilities are
+// already in the B-operand layout of the second product O^T = V^T P^T (lane l supplies column
+// n = l % 32 = its row; its 8 k-slots are 8 of its own keys). P never leaves registers -- the
+// smem round trips the reference's WMMA kernels need (ref:src/stage5_tuned.cu:63-76) do not exist.
+// The price is that V must be read "transposed" (8 keys of one head-dim column per lane): V^T is
+// therefore what the tile loader writes to LDS, with the keys of each 16-key group permuted
+// (0-3, 8-11, 4-7, 12-15) so every PV operand is one 16-byte LDS read.
+//
+// LDS layout (per buffer): Ks[BC][D + pad] row-major (A operand of S^T: lane reads 16 contiguous
+// bytes of key row l % 32), then Vt[D][BC + pad]. pad = 16 bytes: rows shift by 4 banks, so the
+// 32 lanes reading 32 different rows at the same column hit distinct banks (16 lanes x 16 B per
+// LDS cycle).
+//
+// Work distribution: grid = (N / BR) * B * H workgroups on a 1-D grid. Hardware hands workgroup i
+// to XCD i % 8 (8 XCDs, each with its own L2); the kernel remaps blockIdx so that XCD x receives a
+// contiguous range of (head, q-tile) pairs, i.e. all Q tiles of a head sit on one XCD and its K/V
+// is fetched into one L2. For causal problems the heaviest Q tiles (longest key range) are issued
+// first within each XCD.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <type_traits>
+
+#include "fa_internal.h"
+
+namespace fa {
+namespace kern {
+
+using ::fa::KArgs;
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kNumXcd = 8;
+constexpr float kLn2 = 0.69314718055994531f;
+
+// 2^x on the transcendental unit (v_exp_f32). exp2(-inf) = 0, which the masking relies on.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+// log2(x) on the transcendental unit (v_log_f32).
+__device__ __forceinline__ float log2_hw(float x) { return __builtin_amdgcn_logf(x); }
+
+// ---- element conversions -----------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ float to_f32(T x) {
+  return static_cast<float>(x);
+}
+
+// 8 fp32 probabilities -> one 16-byte MFMA operand of 8 fp16/bf16 (round to nearest even).
+template <typename T>
+__device__ __forceinline__ u32x4 pack8(float p0, float p1, float p2, float p3, float p4, float p5,
+                                       float p6, float p7) {
+  if constexpr (sizeof(T) == 2 && __is_same(T, _Float16)) {
+    f16x8 h = {(_Float16)p0, (_Float16)p1, (_Float16)p2, (_Float16)p3,
+               (_Float16)p4, (_Float16)p5, (_Float16)p6, (_Float16)p7};
+    return __builtin_bit_cast(u32x4, h);
+  } else {
+    bf16x8 h = {(__bf16)p0, (__bf16)p1, (__bf16)p2, (__bf16)p3,
+                (__bf16)p4, (__bf16)p5, (__bf16)p6, (__bf16)p7};
+    return __builtin_bit_cast(u32x4, h);
+  }
+}
+
+// 32x32x16 MFMA on 16-bit operands (8 elements per lane in a/b), fp32 accumulate.
+template <typename T>
+__device__ __forceinline__ f32x16 mma16(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (__is_same(T, _Float16)) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+}
+
+// 32x32x2 MFMA on fp32 operands (one element per lane in a/b).
+__device__ __forceinline__ f32x16 mma32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Position of key kk (0..15) inside its 16-key group in the V^T LDS row: keys 0-3, 8-11, 4-7,
+// 12-15 become positions 0-15, so lane half g of the PV operand reads positions 8g..8g+7, which
+// are exactly the keys 8(i/4) + 4g + i%4 (i = 0..7) its probability registers hold.
+__device__ __forceinline__ int vt_pos16(int kk) {
+  return 8 * ((kk >> 2) & 1) + 4 * (kk >> 3) + (kk & 3);
+}
+
+// Tio: element type in HBM (q/k/v/o). Tc: operand type in LDS / MFMA (== Tio for the matrix-core
+// stages; float for the fp32 rung). WAVES: 32-row query groups per workgroup (BR = 32*WAVES).
+// BC: keys per K/V tile. PREFETCH: double-buffered LDS + register-staged next-tile loads.
+template <typename Tio, typename Tc, int D_, int WAVES, int BC_, bool PREFETCH>
+struct Attn {
+  static constexpr int D = D_;
+  static constexpr int BC = BC_;
+  static constexpr bool kHalf = sizeof(Tc) == 2;
+  static constexpr int kThreads = 64 * WAVES;
+  static constexpr int kBr = 32 * WAVES;
+  static constexpr int kPad = 16 / static_cast<int>(sizeof(Tc));
+  static constexpr int kLdK = D + kPad;  // Ks row stride (elements)
+  static constexpr int kLdV = BC + kPad;  // Vt row stride (elements)
+  static constexpr int kKElems = BC * kLdK;
+  static constexpr int kBufElems = kKElems + D * kLdV;
+  static constexpr int kBufs = PREFETCH ? 2 : 1;
+  static constexpr int kLdsElems = kBufs * kBufElems;
+  static constexpr size_t kLdsBytes = static_cast<size_t>(kLdsElems) * sizeof(Tc);
+  static constexpr int kKB = BC / 32;  // 32-key blocks per tile
+  static constexpr int kDB = D / 32;   // 32-wide head-dim blocks of O^T
+  // Global -> register staging: 16-byte vectors of Tio.
+  static constexpr int kVec = 16 / static_cast<int>(sizeof(Tio));
+  static constexpr int kRowVecs = D / kVec;                 // 16-byte vectors per K/V row
+  static constexpr int kKChunks = BC * kRowVecs;             // one vector per chunk
+  static constexpr int kVChunks = (BC / 4) * kRowVecs;       // 4 keys x one vector per chunk
+  static constexpr int kNK = (kKChunks + kThreads - 1) / kThreads;
+  static constexpr int kNV = (kVChunks + kThreads - 1) / kThreads;
+  // Per-lane Q operand storage: half path D/16 vectors of 8; fp32 path D/2 floats as D/8 x 4.
+  static constexpr int kQVecs = kHalf ? D / 16 : D / 8;
+
+  static_assert(BC % 32 == 0 && BC >= 32 && BC <= 128, "BC must be 32, 64 or 128");
+  static_assert(D == 64 || D == 128, "D must be 64 or 128");
+  static_assert(WAVES >= 1 && WAVES <= 8, "1..8 waves");
+  static_assert(kLdsBytes <= 160 * 1024, "gfx950 LDS is 160 KiB per workgroup");
+  static_assert(!kHalf || __is_same(Tio, Tc), "16-bit operands are the I/O type itself");
+
+  struct Staging {
+    u32x4 kv[kNK];
+    u32x4 vv[kNV][4];
+  };
+
+  // Issue the global loads of K/V tile starting at key k0 into registers. Keys >= N read as 0
+  // (N % 32 == 0 and k0 % 32 == 0, so a 4-key group is either wholly in range or wholly out).
+  __device__ static void load_tile(Staging& st, const Tio* kb, const Tio* vb, int k0, int N,
+                                   int tid) {
+#pragma unroll
+    for (int i = 0; i < kNK; ++i) {
+      const int c = tid + i * kThreads;
+      u32x4 val = {0u, 0u, 0u, 0u};
+      if ((kKChunks % kThreads == 0) || c < kKChunks) {
+        const int key = k0 + c / kRowVecs;
+        const int col = (c % kRowVecs) * kVec;
+        if (key < N) val = *reinterpret_cast<const u32x4*>(kb + static_cast<size_t>(key) * D + col);
+      }
+      st.kv[i] = val;
+    }
+#pragma unroll
+    for (int i = 0; i < kNV; ++i) {
+      const int c = tid + i * kThreads;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) st.vv[i][j] = u32x4{0u, 0u, 0u, 0u};
+      if ((kVChunks % kThreads == 0) || c < kVChunks) {
+        const int key = k0 + 4 * (c / kRowVecs);
+        const int col = (c % kRowVecs) * kVec;
+        if (key < N) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            st.vv[i][j] =
+                *reinterpret_cast<const u32x4*>(vb + static_cast<size_t>(key + j) * D + col);
+          }
+        }
+      }
+    }
+  }
+
+  // Write the staged tile into one LDS buffer: K row-major, V transposed (see header).
+  __device__ static void store_tile(const Staging& st, Tc* buf, int tid) {
+    Tc* Ks = buf;
+    Tc* Vt = buf + kKElems;
+#pragma unroll
+    for (int i = 0; i < kNK; ++i) {
+      const int c = tid + i * kThreads;
+      if ((kKChunks % kThreads == 0) || c < kKChunks) {
+        const int key = c / kRowVecs;
+        const int col = (c % kRowVecs) * kVec;
+        Tc* dst = Ks + key * kLdK + col;
+        if constexpr (__is_same(Tio, Tc)) {
+          *reinterpret_cast<u32x4*>(dst) = st.kv[i];
+        } else {  // fp16 in HBM, fp32 in LDS: 8 values -> two 16-byte writes
+          const f16x8 h = __builtin_bit_cast(f16x8, st.kv[i]);
+          *reinterpret_cast<f32x4*>(dst) = f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+          *reinterpret_cast<f32x4*>(dst + 4) =
+              f32x4{(float)h[4], (float)h[5], (float)h[6], (float)h[7]};
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kNV; ++i) {
+      const int c = tid + i * kThreads;
+      if ((kVChunks % kThreads == 0) || c < kVChunks) {
+        const int key0 = 4 * (c / kRowVecs);  // first of the 4 keys (tile-local)
+        const int d0 = (c % kRowVecs) * kVec;
+        if constexpr (kHalf) {
+          // 4 keys x 8 head-dim values -> 8 rows of V^T, 4 keys (8 bytes) each.
+          const int pos = 16 * (key0 >> 4) + vt_pos16(key0 & 15);
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const uint32_t sel = e ? 0x07060302u : 0x05040100u;
+              const uint32_t lo = __builtin_amdgcn_perm(st.vv[i][1][w], st.vv[i][0][w], sel);
+              const uint32_t hi = __builtin_amdgcn_perm(st.vv[i][3][w], st.vv[i][2][w], sel);
+              *reinterpret_cast<u32x2*>(Vt + (d0 + 2 * w + e) * kLdV + pos) = u32x2{lo, hi};
+            }
+          }
+        } else if constexpr (__is_same(Tio, float)) {
+          // 4 keys x 4 head-dim fp32 values -> 4 rows of V^T (natural key order), 16 bytes each.
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            *reinterpret_cast<f32x4*>(Vt + (d0 + d) * kLdV + key0) =
+                f32x4{__builtin_bit_cast(float, st.vv[i][0][d]),
+                      __builtin_bit_cast(float, st.vv[i][1][d]),
+                      __builtin_bit_cast(float, st.vv[i][2][d]),
+                      __builtin_bit_cast(float, st.vv[i][3][d])};
+          }
+        } else {
+          // fp16 in HBM, fp32 in LDS: 4 keys x 8 head-dim values -> 8 rows of V^T.
+          const f16x8 h0 = __builtin_bit_cast(f16x8, st.vv[i][0]);
+          const f16x8 h1 = __builtin_bit_cast(f16x8, st.vv[i][1]);
+          const f16x8 h2 = __builtin_bit_cast(f16x8, st.vv[i][2]);
+          const f16x8 h3 = __builtin_bit_cast(f16x8, st.vv[i][3]);
+#pragma unroll
+          for (int d = 0; d < 8; ++d) {
+            *reinterpret_cast<f32x4*>(Vt + (d0 + d) * kLdV + key0) =
+                f32x4{(float)h0[d], (float)h1[d], (float)h2[d], (float)h3[d]};
+          }
+        }
+      }
+    }
+  }
+
+  // Per-wave running state: Q operand, O^T accumulator, row max (raw units) and partial row sum
+  // (this lane's half of the row's keys; the two halves are added in the epilogue).
+  struct WaveState {
+    u32x4 qh[kHalf ? kQVecs : 1];
+    f32x4 qf[kHalf ? 1 : kQVecs];
+    f32x16 o[kDB];
+    float m;
+    float l;
+  };
+
+  __device__ static void load_q(WaveState& ws, const Tio* qb, int row, bool valid, int g) {
+    if constexpr (kHalf) {
+#pragma unroll
+      for (int s = 0; s < kQVecs; ++s) {
+        ws.qh[s] = valid ? *reinterpret_cast<const u32x4*>(qb + static_cast<size_t>(row) * D +
+                                                           16 * s + 8 * g)
+                         : u32x4{0u, 0u, 0u, 0u};
+      }
+    } else {
+      // fp32 MFMA k-slot mapping: lane half g covers head-dim [g*D/2, (g+1)*D/2).
+      const Tio* src = qb + static_cast<size_t>(row) * D + g * (D / 2);
+#pragma unroll
+      for (int j = 0; j < kQVecs; ++j) {
+        if (!valid) {
+          ws.qf[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        } else if constexpr (__is_same(Tio, float)) {
+          ws.qf[j] = *reinterpret_cast<const f32x4*>(src + 4 * j);
+        } else {
+          const f16x4 h = *reinterpret_cast<const f16x4*>(src + 4 * j);
+          ws.qf[j] = f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+        }
+      }
+    }
+  }
+
+  // One K/V tile for one wave: nvalid leading 32-key blocks take part; `diag` is the index of
+  // the block on the causal diagonal (-1 if none).
+  __device__ static void compute_tile(WaveState& ws, const Tc* buf, int nvalid, int diag, float c,
+                                      int lane) {
+    const Tc* Ks = buf;
+    const Tc* Vt = buf + kKElems;
+    const int g = lane >> 5;
+    const int r32 = lane & 31;
+    f32x16 s[kKB];
+    // ---- S^T = K Q^T ---------------------------------------------------------------------------
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) {
+      if (kb < nvalid) {
+        f32x16 acc = {};
+        const Tc* krow = Ks + (32 * kb + r32) * kLdK;
+        if constexpr (kHalf) {
+#pragma unroll
+          for (int st = 0; st < D / 16; ++st) {
+            const u32x4 a = *reinterpret_cast<const u32x4*>(krow + 16 * st + 8 * g);
+            acc = mma16<Tc>(a, ws.qh[st], acc);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < kQVecs; ++j) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(krow + g * (D / 2) + 4 * j);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc = mma32(a[e], ws.qf[j][e], acc);
+          }
+        }
+        s[kb] = acc;
+      }
+    }
+    // ---- causal diagonal block: key (8(r/4) + 4g + r%4) > row (r32) is masked ---------------
+    if (diag >= 0) {
+#pragma unroll
+      for (int kb = 0; kb < kKB; ++kb) {
+        if (kb == diag) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = 8 * (r >> 2) + 4 * g + (r & 3);
+            if (key > r32) s[kb][r] = -__builtin_inff();
+          }
+        }
+      }
+    }
+    // ---- online softmax (ref:include/fa/softmax_math.cuh:25-71) ------------------------------
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) {
+      if (kb < nvalid) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(ws.m, mx);
+    // Guard: a row with no visible key so far keeps m = -inf; subtracting 0 instead keeps every
+    // masked p = exp2(-inf) = 0 and alpha = 0 (acc and l are still 0), never NaN.
+    const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
+    const float alpha = exp2_hw((ws.m - m_use) * c);
+    const float mc = m_use * c;
+    float rs = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) {
+      if (kb < nvalid) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = exp2_hw(__builtin_fmaf(s[kb][r], c, -mc));
+          s[kb][r] = p;
+          rs += p;
+        }
+      }
+    }
+    ws.l = ws.l * alpha + rs;
+    ws.m = m_new;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) ws.o[db] *= alpha;
+    // ---- O^T += V^T P^T ------------------------------------------------------------------------
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) {
+      if (kb < nvalid) {
+        if constexpr (kHalf) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const u32x4 pf = pack8<Tc>(s[kb][8 * h + 0], s[kb][8 * h + 1], s[kb][8 * h + 2],
+                                       s[kb][8 * h + 3], s[kb][8 * h + 4], s[kb][8 * h + 5],
+                                       s[kb][8 * h + 6], s[kb][8 * h + 7]);
+#pragma unroll
+            for (int db = 0; db < kDB; ++db) {
+              const u32x4 a = *reinterpret_cast<const u32x4*>(Vt + (32 * db + r32) * kLdV +
+                                                              32 * kb + 16 * h + 8 * g);
+              ws.o[db] = mma16<Tc>(a, pf, ws.o[db]);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int db = 0; db < kDB; ++db) {
+              const f32x4 a = *reinterpret_cast<const f32x4*>(Vt + (32 * db + r32) * kLdV +
+                                                              32 * kb + 8 * j + 4 * g);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) ws.o[db] = mma32(a[e], s[kb][4 * j + e], ws.o[db]);
+            }
+          }
+        }
+      }
+    }
+  }
+
+  __device__ static void run(const KArgs& a) {
+    __shared__ __attribute__((aligned(16))) Tc lds[kLdsElems];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int g = lane >> 5;
+
+    // XCD-aware remap of the 1-D grid (see header), then (head, q-tile) decode.
+    const int G = gridDim.x;
+    const int bid = blockIdx.x;
+    const int xcd = bid % kNumXcd;
+    const int per = G / kNumXcd;
+    const int rem = G % kNumXcd;
+    const int logical =
+        (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + bid / kNumXcd;
+    const int bh = logical / a.n_qtiles;
+    int qt = logical - bh * a.n_qtiles;
+    if (a.causal) qt = a.n_qtiles - 1 - qt;  // longest key ranges first
+    const int b = bh / a.H;
+    const int h = bh - b * a.H;
+    const int hk = h / (a.H / a.Hkv);
+    const int N = a.N;
+
+    const size_t q_off = (static_cast<size_t>(b) * a.H + h) * static_cast<size_t>(N) * D;
+    const size_t kv_off = (static_cast<size_t>(b) * a.Hkv + hk) * static_cast<size_t>(N) * D;
+    const Tio* qb = static_cast<const Tio*>(a.q) + q_off;
+    const Tio* kb = static_cast<const Tio*>(a.k) + kv_off;
+    const Tio* vb = static_cast<const Tio*>(a.v) + kv_off;
+
+    const int i0 = qt * kBr;
+    const int r0 = i0 + 32 * wave;  // this wave's first row
+    const bool wave_valid = r0 < N;
+    const int row = r0 + (lane & 31);
+
+    // Key range of the workgroup: causal stops at its last row (tiles beyond are never loaded).
+    const int kv_end = a.causal ? min(N, i0 + kBr) : N;
+    const int n_tiles = (kv_end + BC - 1) / BC;
+    // Key range of this wave (exclusive end), in whole 32-key blocks.
+    const int wave_end = wave_valid ? (a.causal ? min(N, r0 + 32) : N) : 0;
+
+    WaveState ws;
+    load_q(ws, qb, row, wave_valid, g);
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) ws.o[db] = f32x16{};
+    ws.m = -__builtin_inff();
+    ws.l = 0.f;
+
+    Staging st;
+    if constexpr (PREFETCH) {
+      load_tile(st, kb, vb, 0, N, tid);
+      store_tile(st, lds, tid);
+      __syncthreads();
+      for (int t = 0; t < n_tiles; ++t) {
+        const int k0 = t * BC;
+        if (t + 1 < n_tiles) load_tile(st, kb, vb, k0 + BC, N, tid);
+        const int nvalid = max(0, min(kKB, (wave_end - k0 + 31) / 32));
+        if (nvalid > 0) {
+          const int diag = a.causal ? (r0 - k0) / 32 : -1;  // r0, k0 multiples of 32
+          compute_tile(ws, lds + (t & 1) * kBufElems, nvalid,
+                       (diag >= 0 && diag < nvalid) ? diag : -1, a.c, lane);
+        }
+        if (t + 1 < n_tiles) store_tile(st, lds + ((t + 1) & 1) * kBufElems, tid);
+        __syncthreads();
+      }
+    } else {
+      for (int t = 0; t < n_tiles; ++t) {
+        const int k0 = t * BC;
+        load_tile(st, kb, vb, k0, N, tid);
+        store_tile(st, lds, tid);
+        __syncthreads();
+        const int nvalid = max(0, min(kKB, (wave_end - k0 + 31) / 32));
+        if (nvalid > 0) {
+          const int diag = a.causal ? (r0 - k0) / 32 : -1;
+          compute_tile(ws, lds, nvalid, (diag >= 0 && diag < nvalid) ? diag : -1, a.c, lane);
+        }
+        __syncthreads();
+      }
+    }
+
+    // ---- epilogue: O = acc / l, lse = m*scale + ln l (ref:include/fa/softmax_math.cuh:58-71) --
+    const float lt = ws.l + __shfl_xor(ws.l, 32);
+    if (!wave_valid) return;
+    const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
+    Tio* orow = static_cast<Tio*>(a.o) + q_off + static_cast<size_t>(row) * D;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = 32 * db + 8 * j + 4 * g;
+        const float x0 = ws.o[db][4 * j + 0] * inv, x1 = ws.o[db][4 * j + 1] * inv;
+        const float x2 = ws.o[db][4 * j + 2] * inv, x3 = ws.o[db][4 * j + 3] * inv;
+        if constexpr (__is_same(Tio, float)) {
+          *reinterpret_cast<f32x4*>(orow + d) = f32x4{x0, x1, x2, x3};
+        } else if constexpr (__is_same(Tio, _Float16)) {
+          *reinterpret_cast<f16x4*>(orow + d) =
+              f16x4{(_Float16)x0, (_Float16)x1, (_Float16)x2, (_Float16)x3};
+        } else {
+          *reinterpret_cast<bf16x4*>(orow + d) = bf16x4{(__bf16)x0, (__bf16)x1, (__bf16)x2, (__bf16)x3};
+        }
+      }
+    }
+    if (g == 0) {
+      a.lse[(static_cast<size_t>(b) * a.H + h) * static_cast<size_t>(N) + row] =
+          (lt > 0.f && ws.m != -__builtin_inff()) ? ws.m * a.scale + log2_hw(lt) * kLn2
+                                                   : __builtin_inff();
+    }
+  }
+};
+
+// Kernel entry points; the names are the profiler-visible identifiers of the three stage slots.
+template <typename T, int D, int WAVES, int BC>
+__global__ __launch_bounds__(64 * WAVES) void fa_s5_tuned(KArgs a) {
+  Attn<T, T, D, WAVES, BC, true>::run(a);
+}
+
+template <typename T, int D, int WAVES, int BC>
+__global__ __launch_bounds__(64 * WAVES) void fa_s4_mfma(KArgs a) {
+  Attn<T, T, D, WAVES, BC, false>::run(a);
+}
+
+template <typename T, int D, int WAVES, int BC>
+__global__ __launch_bounds__(64 * WAVES) void fa_s3_fused(KArgs a) {
+  Attn<T, float, D, WAVES, BC, true>::run(a);
+}
+
+// Host-side launch of one instantiated variant. STAGE selects the kernel entry point.
+template <int STAGE, typename T, int D, int WAVES, int BC>
+int launch(const KArgs& in, hipStream_t stream) {
+  using A = Attn<T, std::conditional_t<STAGE == 3, float, T>, D, WAVES, BC, STAGE != 4>;
+  KArgs a = in;
+  a.n_qtiles = (a.N + A::kBr - 1) / A::kBr;
+  const long long grid = static_cast<long long>(a.n_qtiles) * a.B * a.H;
+  if (grid <= 0 || grid > 0x7fffffffLL) return static_cast<int>(hipErrorInvalidValue);
+  const dim3 g(static_cast<unsigned>(grid)), b(A::kThreads);
+  if constexpr (STAGE == 5) {
+    hipLaunchKernelGGL((fa_s5_tuned<T, D, WAVES, BC>), g, b, 0, stream, a);
+  } else if constexpr (STAGE == 4) {
+    hipLaunchKernelGGL((fa_s4_mfma<T, D, WAVES, BC>), g, b, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((fa_s3_fused<T, D, WAVES, BC>), g, b, 0, stream, a);
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
+template <int STAGE, typename T, int D, int WAVES, int BC>
+constexpr Variant variant() {
+  return Variant{D, 32 * WAVES, BC, &launch<STAGE, T, D, WAVES, BC>};
+}
+
+// ---- instantiation tables ------------------------------------------------------------------
+// Stage 5: query-tile heights BR = 32..256 and key tiles BC = 32..128 (the sweep / tile-invariance
+// set); defaults are chosen by the host launcher. Stage 4: BR fixed at 128, BC in {32, 64, 128}.
+// Stage 3: BR fixed at 128, BC in {32, 64}.
+template <typename T, int D>
+struct S5Rows {
+  static constexpr Variant rows[] = {
+      variant<5, T, D, 1, 32>(), variant<5, T, D, 1, 64>(),  variant<5, T, D, 2, 32>(),
+      variant<5, T, D, 2, 64>(), variant<5, T, D, 4, 32>(),  variant<5, T, D, 4, 64>(),
+      variant<5, T, D, 4, 128>(), variant<5, T, D, 8, 64>()};
+};
+
+template <typename T>
+VariantList s5_table() {
+  static const Variant t[] = {
+      S5Rows<T, 64>::rows[0],  S5Rows<T, 64>::rows[1],  S5Rows<T, 64>::rows[2],
+      S5Rows<T, 64>::rows[3],  S5Rows<T, 64>::rows[4],  S5Rows<T, 64>::rows[5],
+      S5Rows<T, 64>::rows[6],  S5Rows<T, 64>::rows[7],  S5Rows<T, 128>::rows[0],
+      S5Rows<T, 128>::rows[1], S5Rows<T, 128>::rows[2], S5Rows<T, 128>::rows[3],
+      S5Rows<T, 128>::rows[4], S5Rows<T, 128>::rows[5], S5Rows<T, 128>::rows[6],
+      S5Rows<T, 128>::rows[7]};
+  return VariantList{t, static_cast<int>(sizeof(t) / sizeof(t[0]))};
+}
+
+template <typename T>
+VariantList s4_table() {
+  static const Variant t[] = {variant<4, T, 64, 4, 32>(),  variant<4, T, 64, 4, 64>(),
+                              variant<4, T, 64, 4, 128>(), variant<4, T, 128, 4, 32>(),
+                              variant<4, T, 128, 4, 64>(), variant<4, T, 128, 4, 128>()};
+  return VariantList{t, static_cast<int>(sizeof(t) / sizeof(t[0]))};
+}
+
+template <typename T>
+VariantList s3_table() {
+  static const Variant t[] = {variant<3, T, 64, 4, 32>(), variant<3, T, 64, 4, 64>(),
+                              variant<3, T, 128, 4, 32>(), variant<3, T, 128, 4, 64>()};
+  return VariantList{t, static_cast<int>(sizeof(t) / sizeof(t[0]))};
+}
+
+}  // namespace kern
+}  // namespace fa

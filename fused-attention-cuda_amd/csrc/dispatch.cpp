@@ -1,0 +1,401 @@
+// dispatch.cpp -- implements every function of include/fa/attention.h: the C-ABI launcher that
+// replaces the reference's stage registry (ref:src/dispatch.cu) and the host halves of its stage
+// launchers (ref:src/stage3_fused.cu:500-616, ref:src/stage4_wmma.cu:660-745,
+// ref:src/stage5_tuned.cu:755-1037). The only file that knows which stages exist.
+//
+// Registry (ref:src/dispatch.cu:44-62): stages 1-2 (the materialising ladder rungs) are not built,
+// so fa_impl_supports() reports false for them and fa_forward returns hipErrorNotSupported, the
+// reference's behaviour for an unregistered stage. Stages 3, 4, 5 map to the kernels of
+// attn_kernel.h through the per-dtype variant tables of attn_{f32,f16,bf16}.hip.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+#include "fa/attention.h"
+#include "fa_internal.h"
+
+namespace fa {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct StageEntry {
+  int impl;
+  StageForwardFn forward;    // nullptr = not implemented in this build
+  StageSupportsFn supports;  // nullptr = never supported
+};
+
+// ======================= STAGE REGISTRY (one line per stage) =================================
+const StageEntry kStages[] = {
+    {FA_IMPL_NAIVE, nullptr, nullptr},                     // S1: not built (materialising rung)
+    {FA_IMPL_TILED, nullptr, nullptr},                     // S2: not built (materialising rung)
+    {FA_IMPL_FUSED, stage3::forward, stage3::supports},    // fa_s3_fused (fp32 compute)
+    {FA_IMPL_WMMA, stage4::forward, stage4::supports},     // fa_s4_mfma  (synchronous staging)
+    {FA_IMPL_TUNED, stage5::forward, stage5::supports},    // fa_s5_tuned (prefetched staging)
+};
+// ============================================================================================
+
+const StageEntry* find_stage(int impl) {
+  for (const StageEntry& e : kStages) {
+    if (e.impl == impl) return &e;
+  }
+  return nullptr;
+}
+
+// Contract-level gate (ref:src/dispatch.cu:74-89): D in {64, 128}; naive/tiled/fused take
+// fp32/fp16; wmma/tuned take fp16/bf16. Matrix-core stages need gfx950 here.
+bool contract_allows(int impl, int dtype, int D, int arch) {
+  if (D != 64 && D != 128) return false;
+  if (arch != kArchGfx950) return false;
+  switch (impl) {
+    case FA_IMPL_NAIVE:
+    case FA_IMPL_TILED:
+    case FA_IMPL_FUSED:
+      return dtype == FA_DTYPE_F32 || dtype == FA_DTYPE_F16;
+    case FA_IMPL_WMMA:
+    case FA_IMPL_TUNED:
+      return dtype == FA_DTYPE_F16 || dtype == FA_DTYPE_BF16;
+    default:
+      return false;
+  }
+}
+
+// Returns nullptr when valid, else the reason (printed only under FA_VERBOSE);
+// ref:src/dispatch.cu:96-111. Runs before any HIP call, so it needs no device.
+const char* validate(int dtype, const void* q, const void* k, const void* v, const void* o,
+                     const float* lse, const fa_params* p, int impl) {
+  if (p == nullptr) return "params must be non-null";
+  if (p->B <= 0 || p->H <= 0 || p->Hkv <= 0 || p->N <= 0 || p->D <= 0)
+    return "B,H,Hkv,N,D must be > 0";
+  if (p->D != 64 && p->D != 128) return "D must be 64 or 128";
+  if (p->N % 32 != 0) return "N % 32 != 0 (ragged N is a documented limitation)";
+  if (p->H % p->Hkv != 0) return "H % Hkv != 0";
+  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr)
+    return "q/k/v/o must be non-null";
+  if (fa_dtype_size(dtype) == 0) return "unknown dtype";
+  if (lse == nullptr && impl != FA_IMPL_NAIVE && impl != FA_IMPL_TILED)
+    return "lse must be non-null";
+  return nullptr;
+}
+
+// Parses a positive integer from the environment; 0 when unset, empty or malformed (a malformed
+// value is reported so a typo cannot silently test nothing; ref:src/dispatch.cu:122-134).
+int env_positive_int(const char* name) {
+  const char* s = std::getenv(name);
+  if (s == nullptr || *s == '\0') return 0;
+  char* end = nullptr;
+  const long v = std::strtol(s, &end, 10);
+  if (end == s || *end != '\0' || v <= 0 || v > (1 << 20)) {
+    std::fprintf(stderr, "fa: ignoring %s='%s' (expected a positive integer)\n", name, s);
+    return 0;
+  }
+  return static_cast<int>(v);
+}
+
+Overrides g_overrides;  // fa_set_debug_overrides() state; env values layer on top
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<std::uintptr_t>(ptr) & 15u) == 0; }
+
+// Per-device cache of the gfx number (one hipGetDeviceProperties per device per process).
+std::atomic<int> g_arch_cache[64];
+
+int parse_gfx(const char* name) {
+  if (std::strncmp(name, "gfx", 3) != 0) return 0;
+  int v = 0;
+  for (const char* c = name + 3; *c >= '0' && *c <= '9'; ++c) v = v * 10 + (*c - '0');
+  return v;
+}
+
+Overrides overrides_now() {
+  Overrides r = g_overrides;
+  // Environment wins so tests can steer a process without code changes (ref:src/dispatch.cu:181-189).
+  if (const int br = env_positive_int("FA_FORCE_BR")) r.block_m = br;
+  if (const int bc = env_positive_int("FA_FORCE_BC")) r.block_n = bc;
+  return r;
+}
+
+// Checks shared by the three fused stages (ref:src/stage5_tuned.cu:983-1016).
+int common_stage_checks(const char* tag, const void* q, const void* k, const void* v,
+                        const void* o, const float* lse, const fa_params& p) {
+  if (lse == nullptr) {
+    if (verbose()) std::fprintf(stderr, "fa::%s: lse must be non-null (fused stages)\n", tag);
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  if (p.N % 32 != 0 || p.H % p.Hkv != 0) {
+    if (verbose()) std::fprintf(stderr, "fa::%s: N %% 32 != 0 or H %% Hkv != 0\n", tag);
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  if (static_cast<long long>(p.B) * p.H > 65535LL) {
+    if (verbose()) {
+      std::fprintf(stderr, "fa::%s: B*H = %lld exceeds 65535\n", tag,
+                   static_cast<long long>(p.B) * p.H);
+    }
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  // Masking happens on raw scores before the fold into c = scale*log2e; a non-positive or
+  // non-finite scale would turn the -inf sentinel into +inf/NaN.
+  if (!(p.scale > 0.0f) || !std::isfinite(p.scale)) {
+    if (verbose()) std::fprintf(stderr, "fa::%s: scale must be finite and > 0\n", tag);
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) {
+    if (verbose()) std::fprintf(stderr, "fa::%s: q/k/v/o must be 16-byte aligned\n", tag);
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  return static_cast<int>(hipSuccess);
+}
+
+KArgs make_args(const void* q, const void* k, const void* v, void* o, float* lse,
+                const fa_params& p) {
+  KArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  a.B = p.B;
+  a.H = p.H;
+  a.Hkv = p.Hkv;
+  a.N = p.N;
+  a.n_qtiles = 0;
+  a.scale = p.scale;
+  a.c = p.scale * kLog2e;  // folded once per launch (ref:include/fa/softmax_math.cuh:29-32)
+  a.causal = p.causal ? 1 : 0;
+  return a;
+}
+
+const Variant* find_variant(VariantList list, int D, int br, int bc) {
+  for (int i = 0; i < list.n; ++i) {
+    const Variant& e = list.v[i];
+    if (e.D == D && e.br == br && e.bc == bc) return &e;
+  }
+  return nullptr;
+}
+
+void print_valid_set(const char* tag, VariantList list, int D) {
+  std::fprintf(stderr, "fa::%s: instantiated (FA_FORCE_BR, FA_FORCE_BC) for D=%d:", tag, D);
+  for (int i = 0; i < list.n; ++i) {
+    if (list.v[i].D == D) std::fprintf(stderr, " (%d,%d)", list.v[i].br, list.v[i].bc);
+  }
+  std::fprintf(stderr, "\n");
+}
+
+int launch_selected(const char* tag, VariantList list, int br, int bc, const KArgs& a, int D,
+                    hipStream_t stream) {
+  const Variant* e = find_variant(list, D, br, bc);
+  if (e == nullptr) {
+    if (verbose()) {
+      std::fprintf(stderr, "fa::%s: D=%d BR=%d BC=%d is not an instantiated variant\n", tag, D, br,
+                   bc);
+      print_valid_set(tag, list, D);
+    }
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  return e->fn(a, stream);
+}
+
+// Workgroup height / key tile defaults per stage (overridable by FA_FORCE_BR/BC where the
+// stage honours them). BR = 128 rows = 4 waves of 32 rows; BC = 64 keys per K/V tile.
+constexpr int kDefaultBr = 128;
+constexpr int kDefaultBcMfma = 64;
+constexpr int kDefaultBcF32 = 32;
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------
+// Stage 5: matrix-core kernel, register-prefetched double-buffered K/V (fa_s5_tuned).
+namespace stage5 {
+bool supports(int dtype, int D, int arch) {
+  return (D == 64 || D == 128) && arch == kArchGfx950 &&
+         (dtype == FA_DTYPE_F16 || dtype == FA_DTYPE_BF16);
+}
+
+int forward(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+            const fa_params& p, const Overrides& dbg, int arch, hipStream_t stream) {
+  if (!supports(dtype, p.D, arch)) return static_cast<int>(hipErrorNotSupported);
+  const int rc = common_stage_checks("stage5", q, k, v, o, lse, p);
+  if (rc != 0) return rc;
+  const int br = dbg.block_m != 0 ? dbg.block_m : kDefaultBr;
+  const int bc = dbg.block_n != 0 ? dbg.block_n : kDefaultBcMfma;
+  const KArgs a = make_args(q, k, v, o, lse, p);
+  const VariantList list = dtype == FA_DTYPE_F16 ? variants_s5_f16() : variants_s5_bf16();
+  return launch_selected("stage5", list, br, bc, a, p.D, stream);
+}
+}  // namespace stage5
+
+// ---------------------------------------------------------------------------------------------
+// Stage 4: the same kernel with synchronous K/V staging (fa_s4_mfma). BR is fixed, as in the
+// reference's S4 (ref:src/stage4_wmma.cu:716-727): FA_FORCE_BR is ignored, FA_FORCE_BC honoured.
+namespace stage4 {
+bool supports(int dtype, int D, int arch) { return stage5::supports(dtype, D, arch); }
+
+int forward(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+            const fa_params& p, const Overrides& dbg, int arch, hipStream_t stream) {
+  if (!supports(dtype, p.D, arch)) return static_cast<int>(hipErrorNotSupported);
+  const int rc = common_stage_checks("stage4", q, k, v, o, lse, p);
+  if (rc != 0) return rc;
+  if (dbg.block_m != 0 && dbg.block_m != kDefaultBr && verbose()) {
+    std::fprintf(stderr, "fa::stage4: FA_FORCE_BR=%d ignored (BR is fixed at %d)\n", dbg.block_m,
+                 kDefaultBr);
+  }
+  const int bc = dbg.block_n != 0 ? dbg.block_n : kDefaultBcMfma;
+  const KArgs a = make_args(q, k, v, o, lse, p);
+  const VariantList list = dtype == FA_DTYPE_F16 ? variants_s4_f16() : variants_s4_bf16();
+  return launch_selected("stage4", list, kDefaultBr, bc, a, p.D, stream);
+}
+}  // namespace stage4
+
+// ---------------------------------------------------------------------------------------------
+// Stage 3: the fp32-compute rung (fa_s3_fused), fp32 or fp16 I/O. BR fixed (ref:src/stage3_fused.cu:
+// 585-597 ignores FA_FORCE_BR the same way); FA_FORCE_BC in {32, 64}.
+namespace stage3 {
+bool supports(int dtype, int D, int arch) {
+  return (D == 64 || D == 128) && arch == kArchGfx950 &&
+         (dtype == FA_DTYPE_F32 || dtype == FA_DTYPE_F16);
+}
+
+int forward(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+            const fa_params& p, const Overrides& dbg, int arch, hipStream_t stream) {
+  if (!supports(dtype, p.D, arch)) return static_cast<int>(hipErrorNotSupported);
+  const int rc = common_stage_checks("stage3", q, k, v, o, lse, p);
+  if (rc != 0) return rc;
+  if (dbg.block_m != 0 && dbg.block_m != kDefaultBr && verbose()) {
+    std::fprintf(stderr, "fa::stage3: FA_FORCE_BR=%d ignored (BR is fixed at %d)\n", dbg.block_m,
+                 kDefaultBr);
+  }
+  const int bc = dbg.block_n != 0 ? dbg.block_n : kDefaultBcF32;
+  const KArgs a = make_args(q, k, v, o, lse, p);
+  const VariantList list = dtype == FA_DTYPE_F32 ? variants_s3_f32() : variants_s3_f16();
+  return launch_selected("stage3", list, kDefaultBr, bc, a, p.D, stream);
+}
+}  // namespace stage3
+
+}  // namespace fa
+
+// =============================================================================================
+// C-ABI (include/fa/attention.h)
+// =============================================================================================
+extern "C" {
+
+int fa_current_arch(int* arch) {
+  if (arch == nullptr) return static_cast<int>(hipErrorInvalidValue);
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev >= 0 && dev < 64) {
+    const int cached = fa::g_arch_cache[dev].load(std::memory_order_acquire);
+    if (cached != 0) {
+      *arch = cached;
+      return static_cast<int>(hipSuccess);
+    }
+  }
+  hipDeviceProp_t prop;
+  const hipError_t pe = hipGetDeviceProperties(&prop, dev);
+  if (pe != hipSuccess) return static_cast<int>(pe);
+  const int a = fa::parse_gfx(prop.gcnArchName);
+  if (dev >= 0 && dev < 64) fa::g_arch_cache[dev].store(a, std::memory_order_release);
+  *arch = a;
+  return static_cast<int>(hipSuccess);
+}
+
+int fa_forward(int impl, int dtype, const void* q, const void* k, const void* v, void* o,
+               float* lse, void* workspace, const fa_params* p, hipStream_t stream) {
+  if (const char* why = fa::validate(dtype, q, k, v, o, lse, p, impl)) {
+    if (fa::verbose()) std::fprintf(stderr, "fa_forward: invalid params: %s\n", why);
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  int arch = 0;
+  const int rc = fa_current_arch(&arch);
+  if (rc != 0) return rc;
+  const fa::StageEntry* e = fa::find_stage(impl);
+  if (e == nullptr || e->forward == nullptr || !fa_impl_supports(impl, dtype, p->D, arch)) {
+    if (fa::verbose()) {
+      std::fprintf(stderr, "fa_forward: %s/%s/D=%d not supported on gfx%d in this build\n",
+                   fa_impl_name(impl), fa_dtype_name(dtype), p->D, arch);
+    }
+    return static_cast<int>(hipErrorNotSupported);
+  }
+  if (fa_workspace_bytes(impl, dtype, p) > 0 && workspace == nullptr) {
+    if (fa::verbose()) std::fprintf(stderr, "fa_forward: workspace required but NULL\n");
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  return e->forward(dtype, q, k, v, o, lse, *p, fa::overrides_now(), arch, stream);
+}
+
+size_t fa_workspace_bytes(int impl, int /*dtype*/, const fa_params* p) {
+  // Materialising stages keep fp32 S and P (ref:src/dispatch.cu:163-168); fused stages need none.
+  if (p == nullptr || (impl != FA_IMPL_NAIVE && impl != FA_IMPL_TILED)) return 0;
+  const size_t n = static_cast<size_t>(p->N);
+  return 2u * static_cast<size_t>(p->B) * static_cast<size_t>(p->H) * n * n * sizeof(float);
+}
+
+bool fa_impl_supports(int impl, int dtype, int D, int arch) {
+  if (!fa::contract_allows(impl, dtype, D, arch)) return false;
+  const fa::StageEntry* e = fa::find_stage(impl);
+  if (e == nullptr || e->supports == nullptr) return false;
+  return e->supports(dtype, D, arch);
+}
+
+void fa_set_debug_overrides(int block_m, int block_n) {
+  fa::g_overrides.block_m = block_m;
+  fa::g_overrides.block_n = block_n;
+}
+
+void fa_get_debug_overrides(bool from_env, int* block_m, int* block_n) {
+  const fa::Overrides r = from_env ? fa::overrides_now() : fa::g_overrides;
+  if (block_m) *block_m = r.block_m;
+  if (block_n) *block_n = r.block_n;
+}
+
+const char* fa_impl_name(int impl) {
+  switch (impl) {
+    case FA_IMPL_NAIVE:
+      return "naive";
+    case FA_IMPL_TILED:
+      return "tiled";
+    case FA_IMPL_FUSED:
+      return "fused";
+    case FA_IMPL_WMMA:
+      return "wmma";
+    case FA_IMPL_TUNED:
+      return "tuned";
+    default:
+      return "unknown";
+  }
+}
+
+const char* fa_dtype_name(int dtype) {
+  switch (dtype) {
+    case FA_DTYPE_F32:
+      return "fp32";
+    case FA_DTYPE_F16:
+      return "fp16";
+    case FA_DTYPE_BF16:
+      return "bf16";
+    default:
+      return "unknown";
+  }
+}
+
+size_t fa_dtype_size(int dtype) {
+  switch (dtype) {
+    case FA_DTYPE_F32:
+      return 4;
+    case FA_DTYPE_F16:
+    case FA_DTYPE_BF16:
+      return 2;
+    default:
+      return 0;
+  }
+}
+
+const char* fa_error_string(int status) {
+  return hipGetErrorString(static_cast<hipError_t>(status));
+}
+
+}  // extern "C"

@@ -1,0 +1,96 @@
+// fa_internal.h -- host-side internals shared by the C-ABI launcher (dispatch.cpp) and the stage
+// translation units (attn_*.hip). Not part of the public boundary (include/fa/attention.h).
+//
+// Stage ABI: every implemented stage defines, in its own namespace, the same two functions the
+// reference's registry binds (ref:src/dispatch.cu:18-42):
+//   forward():  inputs already validated by fa_forward; launches on `stream`, never synchronises,
+//               returns a hipError_t value.
+//   supports(): the stage's own (dtype, D, arch) gate, ANDed with the contract gate.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdio>
+#include <cstdlib>
+
+#include "fa/attention.h"
+
+namespace fa {
+
+struct Overrides {
+  int block_m = 0;  // forced BR (query rows per workgroup); 0 = default
+  int block_n = 0;  // forced BC (keys per K/V tile); 0 = default
+};
+
+// Arguments of every kernel entry point (one struct in the kernarg segment).
+struct KArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  int B;
+  int H;
+  int Hkv;
+  int N;
+  int n_qtiles;  // ceil(N / BR), filled in by the launcher
+  float scale;   // softmax scale (for lse = m*scale + ln l)
+  float c;       // scale * log2(e), folded into every exp2
+  int causal;
+};
+
+// One instantiated (D, BR, BC) kernel of a stage, and the table of them per (stage, dtype).
+using LaunchFn = int (*)(const KArgs& a, hipStream_t stream);
+struct Variant {
+  int D;
+  int br;  // query rows per workgroup
+  int bc;  // keys per K/V tile
+  LaunchFn fn;
+};
+struct VariantList {
+  const Variant* v;
+  int n;
+};
+VariantList variants_s5_f16();   // attn_f16.hip
+VariantList variants_s4_f16();   // attn_f16.hip
+VariantList variants_s5_bf16();  // attn_bf16.hip
+VariantList variants_s4_bf16();  // attn_bf16.hip
+VariantList variants_s3_f32();   // attn_f32.hip (fp32 I/O)
+VariantList variants_s3_f16();   // attn_f32.hip (fp16 I/O, fp32 compute)
+
+using StageForwardFn = int (*)(int dtype, const void* q, const void* k, const void* v, void* o,
+                               float* lse, const fa_params& p, const Overrides& dbg, int arch,
+                               hipStream_t stream);
+using StageSupportsFn = bool (*)(int dtype, int D, int arch);
+
+#define FA_DECLARE_STAGE(ns)                                                                   \
+  namespace ns {                                                                               \
+  int forward(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,     \
+              const fa_params& p, const Overrides& dbg, int arch, hipStream_t stream);         \
+  bool supports(int dtype, int D, int arch);                                                   \
+  }
+FA_DECLARE_STAGE(stage3)  // attn_f32.hip   fa_s3_fused  : fp32 MFMA compute, fp32/fp16 I/O
+FA_DECLARE_STAGE(stage4)  // attn_f16.hip / attn_bf16.hip fa_s4_mfma : synchronous K/V staging
+FA_DECLARE_STAGE(stage5)  // attn_f16.hip / attn_bf16.hip fa_s5_tuned: register-prefetched K/V
+#undef FA_DECLARE_STAGE
+
+// The only architecture this build emits code objects for.
+constexpr int kArchGfx950 = 950;
+
+// FA_VERBOSE gates every diagnostic line: the library never prints otherwise.
+inline bool verbose() {
+  static const bool v = std::getenv("FA_VERBOSE") != nullptr;
+  return v;
+}
+
+// Same status convention as the reference's FA_CUDA_TRY (ref:include/fa/cuda_check.cuh:27-35):
+// return the first error to the caller, never abort.
+#define FA_HIP_TRY(x)                   \
+  do {                                  \
+    hipError_t fa_err__ = (x);          \
+    if (fa_err__ != hipSuccess) {       \
+      return static_cast<int>(fa_err__); \
+    }                                   \
+  } while (0)
+
+}  // namespace fa

@@ -1,0 +1,113 @@
+"""ctypes binding of ``libfa_hip.so`` -- the C-ABI of include/fa/attention.h.
+
+This is the kind of binding any FFI consumer of the kernel library writes: plain pointers, sizes
+and a POD params struct, no torch types at the boundary. The torch op (``_C``, csrc/ext.cpp) is a
+C++ consumer of the same functions; tests and ``bench.py`` use this module to call the C-ABI
+directly on device buffers owned by torch.
+
+``torch`` is imported first on purpose: PyTorch-ROCm ships its own HIP runtime, and loading it
+before ``libfa_hip.so`` makes the library bind to that same runtime instance (one HIP runtime per
+process, so device pointers and streams from torch are valid here).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libfa_hip.so"
+
+# Codes of include/fa/attention.h (same integers as ref:include/fa/attention.cuh:17-26).
+FA_DTYPE_F32, FA_DTYPE_F16, FA_DTYPE_BF16 = 0, 1, 2
+FA_IMPL_NAIVE, FA_IMPL_TILED, FA_IMPL_FUSED, FA_IMPL_WMMA, FA_IMPL_TUNED = 1, 2, 3, 4, 5
+HIP_SUCCESS, HIP_ERROR_INVALID_VALUE, HIP_ERROR_NOT_SUPPORTED = 0, 1, 801
+
+DTYPE_CODES = {torch.float32: FA_DTYPE_F32, torch.float16: FA_DTYPE_F16,
+               torch.bfloat16: FA_DTYPE_BF16}
+
+# Every function include/fa/attention.h declares, in declaration order.
+EXPORTS = ("fa_forward", "fa_workspace_bytes", "fa_impl_supports", "fa_set_debug_overrides",
+           "fa_get_debug_overrides", "fa_impl_name", "fa_dtype_name", "fa_dtype_size",
+           "fa_current_arch", "fa_error_string")
+
+
+class FaParams(ctypes.Structure):
+    """``fa_params`` (include/fa/attention.h): B, H, Hkv, N, D, scale, causal."""
+
+    _fields_ = [("B", ctypes.c_int), ("H", ctypes.c_int), ("Hkv", ctypes.c_int),
+                ("N", ctypes.c_int), ("D", ctypes.c_int), ("scale", ctypes.c_float),
+                ("causal", ctypes.c_bool)]
+
+
+_lib: ctypes.CDLL | None = None
+
+
+def load(path: Path | None = None) -> ctypes.CDLL:
+    """Load ``libfa_hip.so`` once and declare every prototype of the header."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = path or LIB_PATH
+    if not p.exists():
+        raise ImportError(f"{p} is not built; run `python fused-attention-cuda_amd/build.py`")
+    lib = ctypes.CDLL(str(p))
+    vp, ci = ctypes.c_void_p, ctypes.c_int
+    lib.fa_forward.argtypes = [ci, ci, vp, vp, vp, vp, vp, vp, ctypes.POINTER(FaParams), vp]
+    lib.fa_forward.restype = ci
+    lib.fa_workspace_bytes.argtypes = [ci, ci, ctypes.POINTER(FaParams)]
+    lib.fa_workspace_bytes.restype = ctypes.c_size_t
+    lib.fa_impl_supports.argtypes = [ci, ci, ci, ci]
+    lib.fa_impl_supports.restype = ctypes.c_bool
+    lib.fa_set_debug_overrides.argtypes = [ci, ci]
+    lib.fa_set_debug_overrides.restype = None
+    lib.fa_get_debug_overrides.argtypes = [ctypes.c_bool, ctypes.POINTER(ci), ctypes.POINTER(ci)]
+    lib.fa_get_debug_overrides.restype = None
+    lib.fa_impl_name.argtypes = [ci]
+    lib.fa_impl_name.restype = ctypes.c_char_p
+    lib.fa_dtype_name.argtypes = [ci]
+    lib.fa_dtype_name.restype = ctypes.c_char_p
+    lib.fa_dtype_size.argtypes = [ci]
+    lib.fa_dtype_size.restype = ctypes.c_size_t
+    lib.fa_current_arch.argtypes = [ctypes.POINTER(ci)]
+    lib.fa_current_arch.restype = ci
+    lib.fa_error_string.argtypes = [ci]
+    lib.fa_error_string.restype = ctypes.c_char_p
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def params(B: int, H: int, Hkv: int, N: int, D: int, scale: float, causal: bool) -> FaParams:
+    return FaParams(B, H, Hkv, N, D, float(scale), bool(causal))
+
+
+def current_arch() -> int:
+    a = ctypes.c_int(0)
+    rc = load().fa_current_arch(ctypes.byref(a))
+    if rc != HIP_SUCCESS:
+        raise RuntimeError(f"fa_current_arch failed: {error_string(rc)}")
+    return a.value
+
+
+def error_string(rc: int) -> str:
+    return load().fa_error_string(rc).decode()
+
+
+def forward_raw(impl: int, dtype: int, q: int, k: int, v: int, o: int, lse: int, workspace: int,
+                p: FaParams, stream: int) -> int:
+    """``fa_forward`` on raw device addresses; returns the hipError_t value."""
+    return load().fa_forward(impl, dtype, q, k, v, o, lse, workspace, ctypes.byref(p), stream)
+
+
+def forward(impl: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+            lse: torch.Tensor | None, is_causal: bool, scale: float,
+            stream: torch.cuda.Stream | None = None) -> int:
+    """``fa_forward`` on torch device tensors (caller-allocated o and lse, like any C caller).
+    Launches on ``stream`` (default: torch's current stream) and returns the hipError_t value."""
+    b, h, n, d = q.shape
+    p = params(b, h, k.shape[1], n, d, scale, is_causal)
+    s = stream if stream is not None else torch.cuda.current_stream(q.device)
+    return forward_raw(impl, DTYPE_CODES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                       o.data_ptr(), 0 if lse is None else lse.data_ptr(), 0, p, s.cuda_stream)

@@ -1,0 +1,105 @@
+/* fa/attention.h -- C-ABI of the MI355X (gfx950) fused scaled-dot-product-attention forward.
+ *
+ * This is the drop-in boundary of libfa_hip.so. It restates the reference's frozen C++ kernel API
+ * (ref:include/fa/attention.cuh:13-69, implemented by ref:src/dispatch.cu) as plain `extern "C"`
+ * functions over POD types and a HIP stream, so that any FFI (ctypes, cgo, JNI, a C++ torch
+ * binding) can bind it. Field order, integer codes, layout contract, error semantics and the
+ * stage registry behaviour are the reference's; the names carry an `fa_` prefix instead of the
+ * `fa::` namespace.
+ *
+ * Layout (ref:include/fa/attention.cuh:38-45): q, o are [B, H, N, D] and k, v are [B, Hkv, N, D],
+ * contiguous with D fastest, in the element type `dtype`; lse is [B, H, N] fp32 and holds
+ * m*scale + ln(l) per query row (natural log). Causal masking is top-left aligned (query i sees
+ * keys j <= i). Query head h reads kv head h / (H / Hkv). Default scale is the caller's business
+ * (torch SDPA uses 1/sqrt(D)). N % 32 == 0 and D in {64, 128} are required.
+ *
+ * Errors: functions never abort and never print unless FA_VERBOSE is set. fa_forward returns a
+ * hipError_t value as int: hipSuccess (0); hipErrorInvalidValue for invalid parameters, a forced
+ * tile that is not instantiated, misaligned pointers or a non-positive scale; hipErrorNotSupported
+ * for a (stage, dtype, D, arch) this build does not implement; or the launch error itself.
+ * The launch is asynchronous on `stream` and never synchronises. The library allocates nothing.
+ */
+#ifndef FA_ATTENTION_H_
+#define FA_ATTENTION_H_
+
+#include <hip/hip_runtime_api.h>
+#include <stdbool.h>
+#include <stddef.h>
+
+/* Every entry point below is exported from libfa_hip.so; nothing else is. */
+#ifndef FA_API
+#define FA_API __attribute__((visibility("default")))
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type of q/k/v/o (ref:include/fa/attention.cuh:15-17). Scores, the running max/sum, the
+ * O accumulator and lse are fp32 inside every kernel regardless of dtype. */
+typedef enum fa_dtype { FA_DTYPE_F32 = 0, FA_DTYPE_F16 = 1, FA_DTYPE_BF16 = 2 } fa_dtype;
+
+/* Stage slots, same numbers as the reference ladder (ref:include/fa/attention.cuh:19-26).
+ * This build implements FUSED (3: fp32 compute rung), WMMA (4: the matrix-core kernel with
+ * synchronous K/V staging) and TUNED (5: the matrix-core kernel with register-prefetched K/V). */
+typedef enum fa_impl {
+  FA_IMPL_NAIVE = 1,
+  FA_IMPL_TILED = 2,
+  FA_IMPL_FUSED = 3,
+  FA_IMPL_WMMA = 4,
+  FA_IMPL_TUNED = 5
+} fa_impl;
+
+/* Problem descriptor; same fields, types and order as fa::Params
+ * (ref:include/fa/attention.cuh:28-36). */
+typedef struct fa_params {
+  int B;       /* batch */
+  int H;       /* query heads */
+  int Hkv;     /* key/value heads, H % Hkv == 0 */
+  int N;       /* sequence length (Nq == Nkv), N % 32 == 0 */
+  int D;       /* head dimension, 64 or 128 */
+  float scale; /* softmax scale applied to q.k, finite and > 0 */
+  bool causal; /* top-left aligned causal mask */
+} fa_params;
+
+/* Replaces fa::forward (ref:include/fa/attention.cuh:46-47, ref:src/dispatch.cu:140-161).
+ * Returns a hipError_t value. `lse` must be non-null for stages 3-5. `workspace` may be NULL when
+ * fa_workspace_bytes() is 0 (always, for the stages this build implements). */
+FA_API int fa_forward(int impl, int dtype, const void* q, const void* k, const void* v, void* o,
+               float* lse, void* workspace, const fa_params* p, hipStream_t stream);
+
+/* Replaces fa::workspace_bytes (ref:include/fa/attention.cuh:51, ref:src/dispatch.cu:163-168):
+ * 2*B*H*N*N*4 for the materialising stages 1-2, 0 for the fused stages. */
+FA_API size_t fa_workspace_bytes(int impl, int dtype, const fa_params* p);
+
+/* Replaces fa::impl_supports (ref:include/fa/attention.cuh:56, ref:src/dispatch.cu:170-175).
+ * `arch` is the gfx number of the device as an integer (950 for gfx950) in place of the
+ * reference's compute capability `sm`. */
+FA_API bool fa_impl_supports(int impl, int dtype, int D, int arch);
+
+/* Replaces fa::set_debug_overrides / get_debug_overrides (ref:include/fa/attention.cuh:60-65,
+ * ref:src/dispatch.cu:177-189): forced query-tile height block_m (BR) and key-tile width block_n
+ * (BC), 0 = kernel default. Process-global, not thread-safe (test-only). With from_env true the
+ * environment variables FA_FORCE_BR / FA_FORCE_BC override the programmatic values. */
+FA_API void fa_set_debug_overrides(int block_m, int block_n);
+FA_API void fa_get_debug_overrides(bool from_env, int* block_m, int* block_n);
+
+/* Replaces fa::impl_name / dtype_name / dtype_size (ref:include/fa/attention.cuh:67-69).
+ * Names are the reference's: "naive", "tiled", "fused", "wmma", "tuned"; "fp32", "fp16", "bf16";
+ * "unknown" otherwise. dtype_size is 4, 2, 2, or 0 for an unknown code. */
+FA_API const char* fa_impl_name(int impl);
+FA_API const char* fa_dtype_name(int dtype);
+FA_API size_t fa_dtype_size(int dtype);
+
+/* gfx number of the current HIP device (e.g. 950), the value fa_impl_supports() expects; replaces
+ * the reference's current_sm (ref:src/dispatch.cu:113-120). Returns a hipError_t value. */
+FA_API int fa_current_arch(int* arch);
+
+/* Human-readable text for a status returned by this library (hipGetErrorString). */
+FA_API const char* fa_error_string(int status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_ATTENTION_H_ */

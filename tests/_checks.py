@@ -1,0 +1,52 @@
+"""Tolerance policy and the comparison helper shared by the GPU parity tests.
+
+Two bars, both enforced:
+
+* The build's stated tolerance against the fp64 oracle (north star): O within
+  ``|o - ref| <= atol + rtol * |ref|`` with fp32 (1e-5, 1e-5) and fp16/bf16 (2e-3, 2e-3); LSE within
+  1e-3 absolute.
+* The reference's own gate (ref:tests/test_kernels_gpu.py:34-68): finite output, the
+  FlashAttention ratio rule ``err_mine <= 2 * err_torch + 1e-6`` against torch's unfused attention in
+  the same dtype, and the absolute caps fp32 1e-4 / fp16 1e-2 / bf16 5e-2.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle.oracle import error_ratio, math_reference, to_f64, unfused_reference
+
+O_TOL = {torch.float32: (1e-5, 1e-5), torch.float16: (2e-3, 2e-3), torch.bfloat16: (2e-3, 2e-3)}
+LSE_ATOL = 1e-3
+ABS_CAP = {torch.float32: 1e-4, torch.float16: 1e-2, torch.bfloat16: 5e-2}
+# The reference's LSE tolerance (atol, rtol), ref:tests/test_kernels_gpu.py:36.
+LSE_TOL_REF = {torch.float32: (1e-4, 1e-5), torch.float16: (2e-2, 1e-3),
+               torch.bfloat16: (5e-2, 5e-3)}
+
+
+def assert_close_tol(out, ref64: np.ndarray, atol: float, rtol: float, what: str = "O") -> float:
+    o = to_f64(out)
+    err = np.abs(o - ref64)
+    bound = atol + rtol * np.abs(ref64)
+    worst = float(np.max(err - bound)) if err.size else -1.0
+    assert np.isfinite(o).all(), f"{what}: non-finite values"
+    assert worst <= 0.0, (f"{what}: max |err| {float(err.max()):.3e} exceeds atol {atol} + rtol "
+                          f"{rtol}*|ref| (worst excess {worst:.3e})")
+    return float(err.max()) if err.size else 0.0
+
+
+def check_against_reference(o, q, k, v, causal, dtype, attn_mask=None, scale=None, lse=None):
+    """Ratio rule + caps (reference) and the north-star tolerance; returns the ratio result."""
+    ref64, lse64 = math_reference(q, k, v, is_causal=causal, scale=scale, attn_mask=attn_mask)
+    pt = unfused_reference(q, k, v, is_causal=causal, scale=scale, attn_mask=attn_mask,
+                           device=str(q.device))
+    r = error_ratio(o, ref64, pt)
+    assert r.out_finite, "kernel produced NaN/inf"
+    assert r.ok, f"ratio rule failed: {r}"
+    assert r.err_mine <= ABS_CAP[dtype], f"absolute cap {ABS_CAP[dtype]} exceeded: {r}"
+    atol, rtol = O_TOL[dtype]
+    assert_close_tol(o, ref64, atol, rtol)
+    if lse is not None:
+        assert_close_tol(lse, lse64, LSE_ATOL, 0.0, what="LSE")
+    return r

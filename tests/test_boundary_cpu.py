@@ -1,0 +1,195 @@
+"""CPU tests of the drop-in boundary: libfa_hip.so and the torch binding, without a GPU.
+
+* The C-ABI library loads and exports exactly the functions include/fa/attention.h declares.
+* Host logic that runs before any device call: parameter validation (hipErrorInvalidValue),
+  the stage registry (impl_supports / names / workspace sizes, ref:src/dispatch.cu:56-175) and the
+  debug-override state with its environment layering (ref:src/dispatch.cu:177-189).
+* The torch op schemas are the reference's verbatim (ref:python/fused_attn/ext.cpp:220-230) and the
+  fake kernels give the reference's output metadata (ref:python/fused_attn/ops.py:44-60).
+* The product never reaches the oracle: no product source names it.
+No test here launches a kernel.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+import torch
+
+from fused_attn import capi
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "fa" / "attention.h"
+PKG = ROOT / "fused-attention-cuda_amd"
+
+pytestmark = pytest.mark.skipif(not capi.LIB_PATH.exists(),
+                                reason="libfa_hip.so not built (run __graft_entry__.build())")
+
+
+def header_functions() -> list[str]:
+    text = HEADER.read_text()
+    return re.findall(r"^FA_API\s+[\w\s\*]+?\b(fa_\w+)\(", text, flags=re.M)
+
+
+def test_header_declares_the_capi_exports():
+    assert header_functions() == list(capi.EXPORTS)
+
+
+def test_library_exports_exactly_the_header_functions():
+    lib = capi.load()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(capi.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    text_syms = sorted(line.split()[-1] for line in out.splitlines() if " T " in line)
+    assert text_syms == sorted(header_functions())
+
+
+def test_names_and_sizes():
+    lib = capi.load()
+    assert [lib.fa_impl_name(i).decode() for i in range(0, 7)] == [
+        "unknown", "naive", "tiled", "fused", "wmma", "tuned", "unknown"]
+    assert [lib.fa_dtype_name(i).decode() for i in range(-1, 4)] == [
+        "unknown", "fp32", "fp16", "bf16", "unknown"]
+    assert [lib.fa_dtype_size(i) for i in range(-1, 4)] == [0, 4, 2, 2, 0]
+
+
+def test_workspace_bytes():
+    lib = capi.load()
+    p = capi.params(2, 8, 8, 2048, 64, 0.125, False)
+    assert lib.fa_workspace_bytes(1, 0, p) == 2 * 2 * 8 * 2048 * 2048 * 4
+    assert lib.fa_workspace_bytes(2, 1, p) == 2 * 2 * 8 * 2048 * 2048 * 4
+    for impl in (3, 4, 5):
+        assert lib.fa_workspace_bytes(impl, 1, p) == 0
+
+
+def test_impl_supports_registry():
+    lib = capi.load()
+    f32, f16, bf16 = capi.FA_DTYPE_F32, capi.FA_DTYPE_F16, capi.FA_DTYPE_BF16
+    for d in (64, 128):
+        assert not lib.fa_impl_supports(1, f32, d, 950) and not lib.fa_impl_supports(2, f16, d, 950)
+        assert lib.fa_impl_supports(3, f32, d, 950) and lib.fa_impl_supports(3, f16, d, 950)
+        assert not lib.fa_impl_supports(3, bf16, d, 950)  # contract: fused takes fp32/fp16
+        for s in (4, 5):
+            assert lib.fa_impl_supports(s, f16, d, 950) and lib.fa_impl_supports(s, bf16, d, 950)
+            assert not lib.fa_impl_supports(s, f32, d, 950)
+    assert not lib.fa_impl_supports(5, f16, 96, 950)
+    assert not lib.fa_impl_supports(5, f16, 64, 942)  # code objects are gfx950-only
+    assert not lib.fa_impl_supports(6, f16, 64, 950) and not lib.fa_impl_supports(0, f16, 64, 950)
+
+
+class _Dev:
+    """Fake 16-byte-aligned 'device' addresses: validation must reject before dereferencing."""
+
+    q, k, v, o, lse = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000
+
+
+@pytest.mark.parametrize("field,value", [("B", 0), ("H", -1), ("Hkv", 0), ("N", 0), ("D", 0),
+                                         ("D", 96), ("N", 100), ("Hkv", 4)])
+def test_invalid_params_rejected_before_any_device_call(field, value):
+    p = capi.params(1, 6, 6, 128, 64, 0.125, False)
+    setattr(p, field, value)
+    d = _Dev
+    rc = capi.forward_raw(5, capi.FA_DTYPE_F16, d.q, d.k, d.v, d.o, d.lse, 0, p, 0)
+    assert rc == capi.HIP_ERROR_INVALID_VALUE
+
+
+def test_null_pointers_and_dtype_rejected():
+    p = capi.params(1, 2, 2, 128, 64, 0.125, False)
+    d = _Dev
+    assert capi.forward_raw(5, 1, 0, d.k, d.v, d.o, d.lse, 0, p, 0) == capi.HIP_ERROR_INVALID_VALUE
+    assert capi.forward_raw(5, 1, d.q, d.k, d.v, d.o, 0, 0, p, 0) == capi.HIP_ERROR_INVALID_VALUE
+    assert capi.forward_raw(5, 7, d.q, d.k, d.v, d.o, d.lse, 0, p, 0) == \
+        capi.HIP_ERROR_INVALID_VALUE
+    assert capi.load().fa_forward(5, 1, d.q, d.k, d.v, d.o, d.lse, 0, None, 0) == \
+        capi.HIP_ERROR_INVALID_VALUE
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device path")
+def test_valid_call_without_device_reports_the_hip_error():
+    p = capi.params(1, 2, 2, 128, 64, 0.125, False)
+    d = _Dev
+    rc = capi.forward_raw(5, 1, d.q, d.k, d.v, d.o, d.lse, 0, p, 0)
+    assert rc not in (capi.HIP_SUCCESS, capi.HIP_ERROR_INVALID_VALUE)
+    assert "device" in capi.error_string(rc).lower()
+
+
+def test_debug_overrides_and_env_layering(monkeypatch):
+    lib = capi.load()
+    bm, bn = ctypes.c_int(-1), ctypes.c_int(-1)
+    monkeypatch.delenv("FA_FORCE_BR", raising=False)
+    monkeypatch.delenv("FA_FORCE_BC", raising=False)
+    try:
+        lib.fa_set_debug_overrides(64, 32)
+        lib.fa_get_debug_overrides(True, ctypes.byref(bm), ctypes.byref(bn))
+        assert (bm.value, bn.value) == (64, 32)
+        monkeypatch.setenv("FA_FORCE_BC", "128")
+        lib.fa_get_debug_overrides(True, ctypes.byref(bm), ctypes.byref(bn))
+        assert (bm.value, bn.value) == (64, 128)  # environment wins
+        lib.fa_get_debug_overrides(False, ctypes.byref(bm), ctypes.byref(bn))
+        assert (bm.value, bn.value) == (64, 32)
+        monkeypatch.setenv("FA_FORCE_BR", "abc")  # malformed: ignored (and reported)
+        lib.fa_get_debug_overrides(True, ctypes.byref(bm), ctypes.byref(bn))
+        assert (bm.value, bn.value) == (64, 128)
+    finally:
+        lib.fa_set_debug_overrides(0, 0)
+
+
+# ------------------------------------------------------------------------------------------------
+# torch binding
+# ------------------------------------------------------------------------------------------------
+def test_op_schemas_are_the_references():
+    import fused_attn
+
+    assert fused_attn.is_available()
+    schemas = {str(torch.ops.fused_attn.forward.default._schema),
+               str(torch.ops.fused_attn.forward_stage.default._schema)}
+    assert schemas == {
+        "fused_attn::forward(Tensor q, Tensor k, Tensor v, bool is_causal, float scale) -> Tensor",
+        "fused_attn::forward_stage(Tensor q, Tensor k, Tensor v, bool is_causal, float scale, "
+        "int stage) -> (Tensor, Tensor)",
+    }
+    assert torch.ops.fused_attn.impl_name(5) == "tuned"
+    with pytest.raises(RuntimeError, match="stage must be in 1..5"):
+        torch.ops.fused_attn.impl_name(0)
+    if not torch.cuda.is_available():
+        assert torch.ops.fused_attn.impl_supports(5, "fp16", 64) is False
+
+
+def test_fake_kernels_give_reference_metadata():
+    import fused_attn  # noqa: F401  (registers the fakes)
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        q = torch.empty(2, 4, 256, 64, dtype=torch.float16)
+        o = torch.ops.fused_attn.forward(q, q, q, False, 0.125)
+        assert o.shape == q.shape and o.dtype == q.dtype
+        for stage in (1, 2, 3, 4, 5):
+            o_s, lse = torch.ops.fused_attn.forward_stage(q, q, q, True, 0.125, stage)
+            assert o_s.shape == q.shape
+            assert tuple(lse.shape) == ((2, 4, 256) if stage >= 3 else (0,))
+            assert lse.dtype == torch.float32
+        bad = torch.empty(2, 4, 100, 64, dtype=torch.float16)
+        with pytest.raises(RuntimeError, match="multiple of 32"):
+            torch.ops.fused_attn.forward(bad, bad, bad, False, 0.125)
+
+
+def test_cpu_tensors_are_refused():
+    import fused_attn
+
+    q = torch.randn(1, 2, 64, 64)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        fused_attn.forward(q, q, q)
+
+
+def test_product_sources_never_reach_the_oracle():
+    """The product (kernel library, binding, Python package) must not import, link or call the
+    CPU oracle: parity claims rest on the HIP path being the thing that runs."""
+    for path in list((PKG / "csrc").iterdir()) + list((PKG / "fused_attn").glob("*.py")):
+        if path.suffix in {".h", ".cpp", ".hip", ".py"}:
+            text = path.read_text()
+            assert "oracle" not in text.lower().replace("oracle-free", ""), path
