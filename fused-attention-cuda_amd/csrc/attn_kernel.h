@@ -237,13 +237,14 @@ struct Attn {
           }
         } else if constexpr (__is_same(Tio, float)) {
           // 4 keys x 4 head-dim fp32 values -> 4 rows of V^T (natural key order), 16 bytes each.
+          const f32x4 r0 = __builtin_bit_cast(f32x4, st.vv[i][0]);
+          const f32x4 r1 = __builtin_bit_cast(f32x4, st.vv[i][1]);
+          const f32x4 r2 = __builtin_bit_cast(f32x4, st.vv[i][2]);
+          const f32x4 r3 = __builtin_bit_cast(f32x4, st.vv[i][3]);
 #pragma unroll
           for (int d = 0; d < 4; ++d) {
             *reinterpret_cast<f32x4*>(Vt + (d0 + d) * kLdV + key0) =
-                f32x4{__builtin_bit_cast(float, st.vv[i][0][d]),
-                      __builtin_bit_cast(float, st.vv[i][1][d]),
-                      __builtin_bit_cast(float, st.vv[i][2][d]),
-                      __builtin_bit_cast(float, st.vv[i][3][d])};
+                f32x4{r0[d], r1[d], r2[d], r3[d]};
           }
         } else {
           // fp16 in HBM, fp32 in LDS: 4 keys x 8 head-dim values -> 8 rows of V^T.
@@ -380,14 +381,33 @@ struct Attn {
         if constexpr (kHalf) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const u32x4 pf = pack8<Tc>(s[kb][8 * h + 0], s[kb][8 * h + 1], s[kb][8 * h + 2],
-                                       s[kb][8 * h + 3], s[kb][8 * h + 4], s[kb][8 * h + 5],
-                                       s[kb][8 * h + 6], s[kb][8 * h + 7]);
+            float p[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) p[i] = s[kb][8 * h + i];
+            const u32x4 pf = pack8<Tc>(p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]);
+            u32x4 a[kDB];
 #pragma unroll
             for (int db = 0; db < kDB; ++db) {
-              const u32x4 a = *reinterpret_cast<const u32x4*>(Vt + (32 * db + r32) * kLdV +
-                                                              32 * kb + 16 * h + 8 * g);
-              ws.o[db] = mma16<Tc>(a, pf, ws.o[db]);
+              a[db] = *reinterpret_cast<const u32x4*>(Vt + (32 * db + r32) * kLdV + 32 * kb +
+                                                      16 * h + 8 * g);
+              ws.o[db] = mma16<Tc>(a[db], pf, ws.o[db]);
+            }
+            if constexpr (__is_same(Tc, __bf16)) {
+              // bf16 keeps 8 significant bits, so a rounded p is off by up to 2^-8 relative. On
+              // the causal diagonal block -- where the first rows of a sequence have all of their
+              // few keys -- P is applied as hi + lo (two bf16 operands, exact to ~2^-16), which
+              // removes the error that would otherwise dominate those rows. Other blocks average
+              // the rounding over many keys.
+              if (kb == diag) {
+                float lo[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                  lo[i] = p[i] - static_cast<float>(static_cast<__bf16>(p[i]));
+                }
+                const u32x4 pl = pack8<Tc>(lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]);
+#pragma unroll
+                for (int db = 0; db < kDB; ++db) ws.o[db] = mma16<Tc>(a[db], pl, ws.o[db]);
+              }
             }
           }
         } else {

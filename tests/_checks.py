@@ -4,7 +4,10 @@ Two bars, both enforced:
 
 * The build's stated tolerance against the fp64 oracle (north star): O within
   ``|o - ref| <= atol + rtol * |ref|`` with fp32 (1e-5, 1e-5) and fp16/bf16 (2e-3, 2e-3); LSE within
-  1e-3 absolute.
+  1e-3 absolute. For bf16 the relative term adds bf16's unit roundoff 2^-8 (~3.9e-3): O is stored
+  in the input dtype, and rounding the exact answer to bf16 alone can move it by up to 2^-8 * |O|,
+  more than 2e-3 -- no bf16-output kernel can do better. fp16's unit roundoff (2^-11) fits inside
+  the 2e-3 bar, so fp16 gets no such term.
 * The reference's own gate (ref:tests/test_kernels_gpu.py:34-68): finite output, the
   FlashAttention ratio rule ``err_mine <= 2 * err_torch + 1e-6`` against torch's unfused attention in
   the same dtype, and the absolute caps fp32 1e-4 / fp16 1e-2 / bf16 5e-2.
@@ -17,7 +20,9 @@ import torch
 
 from oracle.oracle import error_ratio, math_reference, to_f64, unfused_reference
 
-O_TOL = {torch.float32: (1e-5, 1e-5), torch.float16: (2e-3, 2e-3), torch.bfloat16: (2e-3, 2e-3)}
+BF16_UNIT_ROUNDOFF = 2.0 ** -8
+O_TOL = {torch.float32: (1e-5, 1e-5), torch.float16: (2e-3, 2e-3),
+         torch.bfloat16: (2e-3, 2e-3 + BF16_UNIT_ROUNDOFF)}
 LSE_ATOL = 1e-3
 ABS_CAP = {torch.float32: 1e-4, torch.float16: 1e-2, torch.bfloat16: 5e-2}
 # The reference's LSE tolerance (atol, rtol), ref:tests/test_kernels_gpu.py:36.
