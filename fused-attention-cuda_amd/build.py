@@ -34,9 +34,12 @@ ARCH = "gfx950"
 # Packed fp32 VALU forms are switched off for all device code (the compiler would otherwise form
 # v_pk_{add,mul,fma}_f32 from scalar float code).
 NO_PACKED_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Keep MFMA accumulators in ordinary VGPRs: the O accumulator is rescaled by VALU every tile, and
+# in AGPRs each rescale costs a v_accvgpr_read + v_accvgpr_write per element.
+MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 HIP_FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
              "-Wall", "-Wno-unused-function",
-             f"-I{INCLUDE}", f"-I{CSRC}", *NO_PACKED_FP32]
+             f"-I{INCLUDE}", f"-I{CSRC}", *NO_PACKED_FP32, *MFMA_VGPR]
 HIP_SOURCES = ["attn_f16.hip", "attn_bf16.hip", "attn_f32.hip"]
 HOST_SOURCES = ["dispatch.cpp"]
 

@@ -69,6 +69,13 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kNumXcd = 8;
 constexpr float kLn2 = 0.69314718055994531f;
+// Lazy rescaling threshold, in exp2 units: probabilities may reach 2^8 before m is moved. bf16
+// uses 0 (exact running max): with 8 significant bits the largest probability must stay exactly
+// 1.0, or its own rounding (2^-9 relative) dominates the error of concentrated rows.
+template <typename Tc>
+constexpr float lazy_log2() {
+  return __is_same(Tc, __bf16) ? 0.0f : 8.0f;
+}
 
 // 2^x on the transcendental unit (v_exp_f32). exp2(-inf) = 0, which the masking relies on.
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -94,6 +101,20 @@ __device__ __forceinline__ u32x4 pack8(float p0, float p1, float p2, float p3, f
                 (__bf16)p4, (__bf16)p5, (__bf16)p6, (__bf16)p7};
     return __builtin_bit_cast(u32x4, h);
   }
+}
+
+// acc + sum of the 8 fp16 values packed in v, as 4 v_dot2c_f32_f16 against (1, 1). The pairs are
+// taken with shufflevector from one whole-vector bit_cast: a bit_cast of a vector element chosen
+// by a loop index is lowered to element 0 by this compiler.
+__device__ __forceinline__ float dot2_ones_f16(u32x4 v, float acc) {
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  const f16x8 h = __builtin_bit_cast(f16x8, v);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 0, 1), one, acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 2, 3), one, acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 4, 5), one, acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 6, 7), one, acc, false);
+  return acc;
 }
 
 // 32x32x16 MFMA on 16-bit operands (8 elements per lane in a/b), fp32 accumulate.
@@ -161,35 +182,32 @@ struct Attn {
     u32x4 vv[kNV][4];
   };
 
-  // Issue the global loads of K/V tile starting at key k0 into registers. Keys >= N read as 0
-  // (N % 32 == 0 and k0 % 32 == 0, so a 4-key group is either wholly in range or wholly out).
+  // Issue the global loads of K/V tile starting at key k0 into registers. Rows of keys >= N
+  // (only in a partial last tile) are never read back from LDS -- their whole 32-key blocks are
+  // skipped by the math -- so instead of zero-filling, the row index is clamped to N-1: every
+  // address stays inside the tensor and the loads need no per-lane branch.
   __device__ static void load_tile(Staging& st, const Tio* kb, const Tio* vb, int k0, int N,
                                    int tid) {
+    const Tio* kt = kb + static_cast<size_t>(k0) * D;
+    const Tio* vt = vb + static_cast<size_t>(k0) * D;
+    const int last = N - 1 - k0;  // last valid tile-local key row (>= BC - 1 for a full tile)
 #pragma unroll
     for (int i = 0; i < kNK; ++i) {
       const int c = tid + i * kThreads;
-      u32x4 val = {0u, 0u, 0u, 0u};
       if ((kKChunks % kThreads == 0) || c < kKChunks) {
-        const int key = k0 + c / kRowVecs;
-        const int col = (c % kRowVecs) * kVec;
-        if (key < N) val = *reinterpret_cast<const u32x4*>(kb + static_cast<size_t>(key) * D + col);
+        const int row = min(c / kRowVecs, last);
+        st.kv[i] = *reinterpret_cast<const u32x4*>(kt + row * D + (c % kRowVecs) * kVec);
       }
-      st.kv[i] = val;
     }
 #pragma unroll
     for (int i = 0; i < kNV; ++i) {
       const int c = tid + i * kThreads;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) st.vv[i][j] = u32x4{0u, 0u, 0u, 0u};
       if ((kVChunks % kThreads == 0) || c < kVChunks) {
-        const int key = k0 + 4 * (c / kRowVecs);
-        const int col = (c % kRowVecs) * kVec;
-        if (key < N) {
+        const int row = 4 * (c / kRowVecs);
+        const Tio* src = vt + (c % kRowVecs) * kVec;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            st.vv[i][j] =
-                *reinterpret_cast<const u32x4*>(vb + static_cast<size_t>(key + j) * D + col);
-          }
+        for (int j = 0; j < 4; ++j) {
+          st.vv[i][j] = *reinterpret_cast<const u32x4*>(src + min(row + j, last) * D);
         }
       }
     }
@@ -268,8 +286,9 @@ struct Attn {
     u32x4 qh[kHalf ? kQVecs : 1];
     f32x4 qf[kHalf ? 1 : kQVecs];
     f32x16 o[kDB];
-    float m;
-    float l;
+    float m;   // running row max, raw score units (may lag the true max: lazy rescaling)
+    float mc;  // m * c with the -inf guard applied (0 while m == -inf)
+    float l;   // this lane's partial row sum, relative to m
   };
 
   __device__ static void load_q(WaveState& ws, const Tio* qb, int row, bool valid, int g) {
@@ -300,7 +319,7 @@ struct Attn {
   // One K/V tile for one wave: nvalid leading 32-key blocks take part; `diag` is the index of
   // the block on the causal diagonal (-1 if none).
   __device__ static void compute_tile(WaveState& ws, const Tc* buf, int nvalid, int diag, float c,
-                                      int lane) {
+                                      float lazy_raw, int lane) {
     const Tc* Ks = buf;
     const Tc* Vt = buf + kKElems;
     const int g = lane >> 5;
@@ -342,7 +361,9 @@ struct Attn {
         }
       }
     }
-    // ---- online softmax (ref:include/fa/softmax_math.cuh:25-71) ------------------------------
+    // ---- online softmax with lazy rescaling (ref:include/fa/softmax_math.cuh:25-71) --------
+    // Row max of this tile: the lane's 16*nvalid scores, then the partner lane (l ^ 32), which
+    // holds the row's other keys.
     float mx = -__builtin_inff();
 #pragma unroll
     for (int kb = 0; kb < kKB; ++kb) {
@@ -352,29 +373,33 @@ struct Attn {
       }
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(ws.m, mx);
-    // Guard: a row with no visible key so far keeps m = -inf; subtracting 0 instead keeps every
-    // masked p = exp2(-inf) = 0 and alpha = 0 (acc and l are still 0), never NaN.
-    const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
-    const float alpha = exp2_hw((ws.m - m_use) * c);
-    const float mc = m_use * c;
-    float rs = 0.f;
+    // The reference recurrence moves m to the row max on every tile and rescales acc and l by
+    // alpha = exp2((m_old - m_new) c). Here m moves only when some row of the wave sees a max
+    // more than lazy_log2<Tc>() (exp2 units) above its current m; otherwise p = exp2(s c - m c)
+    // stays <= 2^lazy_log2 and nothing is rescaled. acc, l and lse are all taken relative to the same m,
+    // so the function is unchanged, and p stays far inside the fp16/bf16/fp32 range. The decision
+    // is one ballot per tile (wave-uniform), so a skipped rescale costs a scalar branch.
+    if (__builtin_amdgcn_ballot_w64(mx > ws.m + lazy_raw) != 0) {
+      const float m_new = fmaxf(ws.m, mx);
+      // Guard: a row with no visible key so far keeps m = -inf; using 0 in the exponent keeps
+      // every masked p = exp2(-inf) = 0 and alpha = 0 (acc and l are still 0), never NaN.
+      const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
+      const float alpha = exp2_hw((ws.m - m_use) * c);
+      ws.l *= alpha;
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) ws.o[db] *= alpha;
+      ws.m = m_new;
+      ws.mc = m_use * c;
+    }
 #pragma unroll
     for (int kb = 0; kb < kKB; ++kb) {
       if (kb < nvalid) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = exp2_hw(__builtin_fmaf(s[kb][r], c, -mc));
-          s[kb][r] = p;
-          rs += p;
-        }
+        for (int r = 0; r < 16; ++r) s[kb][r] = exp2_hw(__builtin_fmaf(s[kb][r], c, -ws.mc));
       }
     }
-    ws.l = ws.l * alpha + rs;
-    ws.m = m_new;
-#pragma unroll
-    for (int db = 0; db < kDB; ++db) ws.o[db] *= alpha;
-    // ---- O^T += V^T P^T ------------------------------------------------------------------------
+    // ---- O^T += V^T P^T, and the row sum ---------------------------------------------------
+    float rs = 0.f;
 #pragma unroll
     for (int kb = 0; kb < kKB; ++kb) {
       if (kb < nvalid) {
@@ -392,12 +417,19 @@ struct Attn {
                                                       16 * h + 8 * g);
               ws.o[db] = mma16<Tc>(a[db], pf, ws.o[db]);
             }
-            if constexpr (__is_same(Tc, __bf16)) {
-              // bf16 keeps 8 significant bits, so a rounded p is off by up to 2^-8 relative. On
-              // the causal diagonal block -- where the first rows of a sequence have all of their
-              // few keys -- P is applied as hi + lo (two bf16 operands, exact to ~2^-16), which
-              // removes the error that would otherwise dominate those rows. Other blocks average
-              // the rounding over many keys.
+            if constexpr (__is_same(Tc, _Float16)) {
+              // fp16: the row sum is taken over the probabilities exactly as they enter the
+              // product (rounded to fp16), two per packed dot2 -- half the adds of fp32 sums,
+              // and numerator and denominator use the same weights.
+              rs = dot2_ones_f16(pf, rs);
+            } else {
+              // bf16 keeps 8 significant bits, so a rounded p is off by up to 2^-8 relative; the
+              // row sum stays in fp32 (the LSE must hold 1e-3). On the causal diagonal block --
+              // where the first rows of a sequence have all of their few keys -- P is applied as
+              // hi + lo (two bf16 operands, exact to ~2^-16), which removes the error that would
+              // otherwise dominate those rows; other blocks average the rounding over many keys.
+#pragma unroll
+              for (int i = 0; i < 8; ++i) rs += p[i];
               if (kb == diag) {
                 float lo[8];
 #pragma unroll
@@ -412,6 +444,8 @@ struct Attn {
           }
         } else {
 #pragma unroll
+          for (int r = 0; r < 16; ++r) rs += s[kb][r];
+#pragma unroll
           for (int j = 0; j < 4; ++j) {
 #pragma unroll
             for (int db = 0; db < kDB; ++db) {
@@ -424,13 +458,16 @@ struct Attn {
         }
       }
     }
+    ws.l += rs;
   }
 
   __device__ static void run(const KArgs& a) {
     __shared__ __attribute__((aligned(16))) Tc lds[kLdsElems];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // readfirstlane makes the wave index (and everything derived from it: the wave's rows, key
+    // range, diagonal block) provably wave-uniform, so per-wave decisions are scalar branches.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5;
 
     // XCD-aware remap of the 1-D grid (see header), then (head, q-tile) decode.
@@ -471,8 +508,10 @@ struct Attn {
 #pragma unroll
     for (int db = 0; db < kDB; ++db) ws.o[db] = f32x16{};
     ws.m = -__builtin_inff();
+    ws.mc = 0.f;
     ws.l = 0.f;
 
+    const float lazy_raw = lazy_log2<Tc>() / a.c;  // lazy-rescale threshold, raw score units
     Staging st;
     if constexpr (PREFETCH) {
       load_tile(st, kb, vb, 0, N, tid);
@@ -485,7 +524,7 @@ struct Attn {
         if (nvalid > 0) {
           const int diag = a.causal ? (r0 - k0) / 32 : -1;  // r0, k0 multiples of 32
           compute_tile(ws, lds + (t & 1) * kBufElems, nvalid,
-                       (diag >= 0 && diag < nvalid) ? diag : -1, a.c, lane);
+                       (diag >= 0 && diag < nvalid) ? diag : -1, a.c, lazy_raw, lane);
         }
         if (t + 1 < n_tiles) store_tile(st, lds + ((t + 1) & 1) * kBufElems, tid);
         __syncthreads();
@@ -499,7 +538,8 @@ struct Attn {
         const int nvalid = max(0, min(kKB, (wave_end - k0 + 31) / 32));
         if (nvalid > 0) {
           const int diag = a.causal ? (r0 - k0) / 32 : -1;
-          compute_tile(ws, lds, nvalid, (diag >= 0 && diag < nvalid) ? diag : -1, a.c, lane);
+          compute_tile(ws, lds, nvalid, (diag >= 0 && diag < nvalid) ? diag : -1, a.c, lazy_raw,
+                       lane);
         }
         __syncthreads();
       }
