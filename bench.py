@@ -222,6 +222,10 @@ def main(argv=None) -> int:
                          "(for profiler runs)")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="target seconds of CPU baseline work (wall ~ this / threads)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="calibration only: launch a plain device-to-device copy of MIB MiB a few "
+                         "times and exit (the known-size reference for rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE scaling)")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; multi-GPU runs are out of scope "
@@ -235,6 +239,15 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py: no HIP device visible", file=sys.stderr)
         return 2
+    if a.copy_probe > 0:
+        n = a.copy_probe << 20
+        src = torch.ones(n // 4, dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "launches": 5}))
+        return 0
     capi.load()
     head, sets, stream, causal, scale = bench_workload(torch, capi, a.workload, a.stage, a.steps,
                                                        a.warmup)

@@ -1,17 +1,12 @@
-// attn_kernel.h -- the gfx950 fused SDPA forward kernel template (device code + launch helper).
+// attn_kernel.h -- the fp32-compute correctness rung of the fused SDPA forward (stage 3).
 //
-// Included by attn_f16.hip, attn_bf16.hip and attn_f32.hip, which instantiate it. One template
-// serves three stage slots of the reference ladder:
-//   fa_s5_tuned<T>   (stage 5)  fp16/bf16 operands on v_mfma_f32_32x32x16_{f16,bf16}, K/V tiles
-//                               double-buffered in LDS with the next tile's global loads issued
-//                               into registers before the current tile's math (the role of the
-//                               reference's PREFETCH knob, ref:src/stage5_tuned.cu:29-47);
-//   fa_s4_mfma<T>    (stage 4)  the same kernel with synchronous staging (one LDS buffer, load ->
-//                               barrier -> math -> barrier), the reference's S4 = S5 with PREFETCH
-//                               off (ref:src/stage5_tuned.cu:1-8);
-//   fa_s3_fused<T>   (stage 3)  the fp32-compute correctness rung: operands are held in LDS as fp32
-//                               and multiplied on v_mfma_f32_32x32x2_f32, so no operand is rounded
-//                               below fp32 (fp32 or fp16 I/O, ref:src/stage3_fused.cu:142-160).
+// Included by attn_f32.hip, which instantiates it for fp32 and fp16 inputs:
+//   fa_s3_fused<T>   (stage 3)  operands are held in LDS as fp32 and multiplied on
+//                               v_mfma_f32_32x32x2_f32, so no operand is rounded below fp32
+//                               (fp32 or fp16 I/O, ref:src/stage3_fused.cu:142-160). K/V tiles are
+//                               double-buffered in LDS with register-staged prefetch.
+// The 16-bit matrix-core stages (4 and 5) live in attn_mfma16.h. The template below still carries
+// its 16-bit operand paths (kHalf); only the fp32-operand instantiation is built.
 //
 // Algorithm (FlashAttention-2 loop order, the reference's recurrence ref:include/fa/softmax_math.cuh):
 // a workgroup owns BR = 32*WAVES query rows of one (b, h); each wave owns 32 rows for the whole
@@ -575,82 +570,35 @@ struct Attn {
   }
 };
 
-// Kernel entry points; the names are the profiler-visible identifiers of the three stage slots.
-template <typename T, int D, int WAVES, int BC>
-__global__ __launch_bounds__(64 * WAVES) void fa_s5_tuned(KArgs a) {
-  Attn<T, T, D, WAVES, BC, true>::run(a);
-}
-
-template <typename T, int D, int WAVES, int BC>
-__global__ __launch_bounds__(64 * WAVES) void fa_s4_mfma(KArgs a) {
-  Attn<T, T, D, WAVES, BC, false>::run(a);
-}
-
+// Kernel entry point of the fp32 rung (profiler-visible name of stage 3).
 template <typename T, int D, int WAVES, int BC>
 __global__ __launch_bounds__(64 * WAVES) void fa_s3_fused(KArgs a) {
   Attn<T, float, D, WAVES, BC, true>::run(a);
 }
 
-// Host-side launch of one instantiated variant. STAGE selects the kernel entry point.
-template <int STAGE, typename T, int D, int WAVES, int BC>
-int launch(const KArgs& in, hipStream_t stream) {
-  using A = Attn<T, std::conditional_t<STAGE == 3, float, T>, D, WAVES, BC, STAGE != 4>;
+// Host-side launch of one instantiated stage-3 variant.
+template <typename T, int D, int WAVES, int BC>
+int launch_s3(const KArgs& in, hipStream_t stream) {
+  using A = Attn<T, float, D, WAVES, BC, true>;
   KArgs a = in;
   a.n_qtiles = (a.N + A::kBr - 1) / A::kBr;
   const long long grid = static_cast<long long>(a.n_qtiles) * a.B * a.H;
   if (grid <= 0 || grid > 0x7fffffffLL) return static_cast<int>(hipErrorInvalidValue);
-  const dim3 g(static_cast<unsigned>(grid)), b(A::kThreads);
-  if constexpr (STAGE == 5) {
-    hipLaunchKernelGGL((fa_s5_tuned<T, D, WAVES, BC>), g, b, 0, stream, a);
-  } else if constexpr (STAGE == 4) {
-    hipLaunchKernelGGL((fa_s4_mfma<T, D, WAVES, BC>), g, b, 0, stream, a);
-  } else {
-    hipLaunchKernelGGL((fa_s3_fused<T, D, WAVES, BC>), g, b, 0, stream, a);
-  }
+  hipLaunchKernelGGL((fa_s3_fused<T, D, WAVES, BC>), dim3(static_cast<unsigned>(grid)),
+                     dim3(A::kThreads), 0, stream, a);
   return static_cast<int>(hipGetLastError());
 }
 
-template <int STAGE, typename T, int D, int WAVES, int BC>
-constexpr Variant variant() {
-  return Variant{D, 32 * WAVES, BC, &launch<STAGE, T, D, WAVES, BC>};
+template <typename T, int D, int WAVES, int BC>
+constexpr Variant variant_s3() {
+  return Variant{D, 32 * WAVES, BC, &launch_s3<T, D, WAVES, BC>};
 }
 
-// ---- instantiation tables ------------------------------------------------------------------
-// Stage 5: query-tile heights BR = 32..256 and key tiles BC = 32..128 (the sweep / tile-invariance
-// set); defaults are chosen by the host launcher. Stage 4: BR fixed at 128, BC in {32, 64, 128}.
 // Stage 3: BR fixed at 128, BC in {32, 64}.
-template <typename T, int D>
-struct S5Rows {
-  static constexpr Variant rows[] = {
-      variant<5, T, D, 1, 32>(), variant<5, T, D, 1, 64>(),  variant<5, T, D, 2, 32>(),
-      variant<5, T, D, 2, 64>(), variant<5, T, D, 4, 32>(),  variant<5, T, D, 4, 64>(),
-      variant<5, T, D, 4, 128>(), variant<5, T, D, 8, 64>()};
-};
-
-template <typename T>
-VariantList s5_table() {
-  static const Variant t[] = {
-      S5Rows<T, 64>::rows[0],  S5Rows<T, 64>::rows[1],  S5Rows<T, 64>::rows[2],
-      S5Rows<T, 64>::rows[3],  S5Rows<T, 64>::rows[4],  S5Rows<T, 64>::rows[5],
-      S5Rows<T, 64>::rows[6],  S5Rows<T, 64>::rows[7],  S5Rows<T, 128>::rows[0],
-      S5Rows<T, 128>::rows[1], S5Rows<T, 128>::rows[2], S5Rows<T, 128>::rows[3],
-      S5Rows<T, 128>::rows[4], S5Rows<T, 128>::rows[5], S5Rows<T, 128>::rows[6],
-      S5Rows<T, 128>::rows[7]};
-  return VariantList{t, static_cast<int>(sizeof(t) / sizeof(t[0]))};
-}
-
-template <typename T>
-VariantList s4_table() {
-  static const Variant t[] = {variant<4, T, 64, 4, 32>(),  variant<4, T, 64, 4, 64>(),
-                              variant<4, T, 64, 4, 128>(), variant<4, T, 128, 4, 32>(),
-                              variant<4, T, 128, 4, 64>(), variant<4, T, 128, 4, 128>()};
-  return VariantList{t, static_cast<int>(sizeof(t) / sizeof(t[0]))};
-}
-
 template <typename T>
 VariantList s3_table() {
-  static const Variant t[] = {variant<3, T, 64, 4, 32>(), variant<3, T, 64, 4, 64>(),
-                              variant<3, T, 128, 4, 32>(), variant<3, T, 128, 4, 64>()};
+  static const Variant t[] = {variant_s3<T, 64, 4, 32>(), variant_s3<T, 64, 4, 64>(),
+                              variant_s3<T, 128, 4, 32>(), variant_s3<T, 128, 4, 64>()};
   return VariantList{t, static_cast<int>(sizeof(t) / sizeof(t[0]))};
 }
 

@@ -5,8 +5,9 @@
 //
 // Registry (ref:src/dispatch.cu:44-62): stages 1-2 (the materialising ladder rungs) are not built,
 // so fa_impl_supports() reports false for them and fa_forward returns hipErrorNotSupported, the
-// reference's behaviour for an unregistered stage. Stages 3, 4, 5 map to the kernels of
-// attn_kernel.h through the per-dtype variant tables of attn_{f32,f16,bf16}.hip.
+// reference's behaviour for an unregistered stage. Stage 3 maps to the fp32 rung of attn_kernel.h
+// and stages 4-5 to the 16-bit matrix-core kernel of attn_mfma16.h, through the per-dtype variant
+// tables of attn_{f32,f16,bf16}.hip.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -200,9 +201,10 @@ int launch_selected(const char* tag, VariantList list, int br, int bc, const KAr
 }
 
 // Workgroup height / key tile defaults per stage (overridable by FA_FORCE_BR/BC where the
-// stage honours them). BR = 128 rows = 4 waves of 32 rows; BC = 64 keys per K/V tile.
+// stage honours them). Matrix-core stages: BR = 128 rows = 4 row groups of 32, BC = 128 keys
+// split in two halves of 64 (8 waves, 2 per SIMD). fp32 rung: 4 waves of 32 rows, BC = 32.
 constexpr int kDefaultBr = 128;
-constexpr int kDefaultBcMfma = 64;
+constexpr int kDefaultBcMfma = 128;
 constexpr int kDefaultBcF32 = 32;
 
 }  // namespace

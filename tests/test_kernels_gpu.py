@@ -27,10 +27,12 @@ STAGE_DTYPES = {
     5: [torch.float16, torch.bfloat16],
 }
 STAGE_DTYPE_PAIRS = [(s, dt) for s in (3, 4, 5) for dt in STAGE_DTYPES[s]]
-# Instantiated (BR, BC) tiles per stage (csrc/attn_kernel.h tables; 0 = default). Stages 3 and 4
-# fix BR at 128 and ignore a forced BR, as the reference's S3/S4 do.
+# Instantiated (BR, BC) tiles per stage (csrc/attn_mfma16.h and csrc/attn_kernel.h tables;
+# 0 = default). Stages 3 and 4 fix BR at 128 and ignore a forced BR, as the reference's S3/S4 do.
 STAGE_BC = {3: {32, 64}, 4: {32, 64, 128}}
-S5_TILES = {(32, 32), (32, 64), (64, 32), (64, 64), (128, 32), (128, 64), (128, 128), (256, 64)}
+S5_TILES = {(32, 32), (32, 64), (64, 32), (64, 64), (64, 128), (128, 32), (128, 64), (128, 128),
+            (256, 64), (256, 128)}
+S5_DEFAULT = (128, 128)
 
 _ids = {torch.float32: "fp32", torch.float16: "fp16", torch.bfloat16: "bf16"}
 
@@ -48,7 +50,7 @@ def require(stage: int, dtype: torch.dtype, head_dim: int) -> None:
 
 def tile_supported(stage: int, bm: int, bn: int) -> bool:
     if stage == 5:
-        return (bm or 128, bn or 64) in S5_TILES
+        return (bm or S5_DEFAULT[0], bn or S5_DEFAULT[1]) in S5_TILES
     return bn == 0 or bn in STAGE_BC[stage]
 
 
