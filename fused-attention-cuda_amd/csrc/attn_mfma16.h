@@ -1,10 +1,13 @@
 // attn_mfma16.h -- the gfx950 fused SDPA forward for 16-bit operands (fp16 / bf16), stages 5 and 4.
 //
 // Included by attn_f16.hip and attn_bf16.hip. Kernel entry points (profiler-visible names):
-//   fa_s5_tuned<T, D, RG, KS, BCW>  stage 5: K/V tiles double-buffered in LDS; the next tile's
-//                                   global loads are issued into registers before the current
-//                                   tile's math (the reference's PREFETCH, ref:src/stage5_tuned.cu:29-47)
-//   fa_s4_mfma<T, D, RG, KS, BCW>   stage 4: the same kernel with one LDS buffer and synchronous
+//   fa_s5_tuned<T, D, RG, KS, BCW>  stage 5: software-pipelined. K and V tiles are double-buffered
+//                                   in LDS, K one tile ahead of V, and iteration t exponentiates
+//                                   tile t while the MFMAs of the next tile's scores run; the
+//                                   global loads of later tiles are issued into registers before
+//                                   the math (the role of the reference's PREFETCH,
+//                                   ref:src/stage5_tuned.cu:29-47)
+//   fa_s4_mfma<T, D, RG, KS, BCW>   stage 4: the same math with one LDS buffer and synchronous
 //                                   staging (load -> barrier -> math -> barrier), the reference's
 //                                   S4 = S5 with PREFETCH off (ref:src/stage5_tuned.cu:1-8)
 //
@@ -51,6 +54,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <type_traits>
 
 #include "fa_internal.h"
 
@@ -72,14 +76,6 @@ typedef s16x4 __attribute__((address_space(3))) lds_s16x4;
 
 constexpr int kNumXcd = 8;
 constexpr float kLn2 = 0.69314718055994531f;
-
-// Lazy rescaling threshold in exp2 units: probabilities may reach 2^8 before the running max m is
-// moved. bf16 uses 0 (exact running max): with 8 significant bits the largest probability must be
-// exactly 1.0, or its own rounding (2^-9 relative) dominates the error of concentrated rows.
-template <typename T>
-constexpr float lazy_log2() {
-  return __is_same(T, __bf16) ? 0.0f : 8.0f;
-}
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float log2_hw(float x) { return __builtin_amdgcn_logf(x); }
@@ -127,69 +123,67 @@ __device__ __forceinline__ u32x2 lds_read_tr(const void* p) {
 }
 
 // T: fp16 or bf16. RG: 32-row groups per workgroup. KS: key splits. BCW: keys per wave per tile.
-template <typename T, int D_, int RG, int KS, int BCW, bool PREFETCH>
+// PIPE: software-pipelined stage-5 loop (see run()); false = the synchronous stage-4 loop.
+template <typename T, int D_, int RG, int KS, int BCW, bool PIPE>
 struct Fa16 {
   static constexpr int D = D_;
+  static constexpr bool kF16 = __is_same(T, _Float16);
   static constexpr int kWaves = RG * KS;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int kBr = 32 * RG;
   static constexpr int BC = KS * BCW;
-  static constexpr int kLdK = D + 8;   // Ks row stride (elements)
-  static constexpr int kLdV = D + 16;  // Vs row stride (elements)
-  static constexpr int kKElems = BC * kLdK;
-  static constexpr int kBufElems = kKElems + BC * kLdV;
-  static constexpr int kBufs = PREFETCH ? 2 : 1;
-  static constexpr size_t kTileBytes = static_cast<size_t>(kBufs) * kBufElems * 2;
+  static constexpr int kLdK = D + 8;   // K row stride (elements)
+  static constexpr int kLdV = D + 16;  // V row stride (elements)
+  static constexpr int kKElems = BC * kLdK;  // one K buffer
+  static constexpr int kVElems = BC * kLdV;  // one V buffer
+  static constexpr int kBufs = PIPE ? 2 : 1;
+  static constexpr size_t kTileBytes = static_cast<size_t>(kBufs) * (kKElems + kVElems) * 2;
   static constexpr int kKB = BCW / 32;  // 32-key blocks per wave and tile
   static constexpr int kDB = D / 32;    // 32-wide head-dim blocks of O^T
-  static constexpr int kRowChunks = D / 8;           // 16-byte chunks per K/V row
-  static constexpr int kChunks = BC * kRowChunks;    // per tensor and tile
+  static constexpr int kRowChunks = D / 8;         // 16-byte chunks per K/V row
+  static constexpr int kChunks = BC * kRowChunks;  // per tensor and tile
   static constexpr int kNC = (kChunks + kThreads - 1) / kThreads;
   // Merge scratch: every non-leading key split writes its O^T registers, m and l per lane.
   static constexpr int kMergeFloats = (kDB * 16 + 2) * 64;
   static constexpr size_t kMergeBytes =
       KS > 1 ? static_cast<size_t>(KS - 1) * RG * kMergeFloats * sizeof(float) : 0;
   static constexpr size_t kLdsBytes = kTileBytes > kMergeBytes ? kTileBytes : kMergeBytes;
+  // fp16 fast path: p = exp2(s c - m c) is used as long as every probability of the tile stays
+  // <= 2^14 (so the fp16 operand, max 65504, cannot overflow); the check is the lane's tile row
+  // sum, which bounds each of its probabilities.
+  static constexpr float kF16SumLimit = 16384.0f;
 
   static_assert(BCW % 32 == 0 && BCW >= 32 && BCW <= 128, "BCW must be 32, 64 or 128");
   static_assert(D == 64 || D == 128, "D must be 64 or 128");
   static_assert(kWaves >= 1 && kWaves <= 16, "1..16 waves");
   static_assert(kLdsBytes <= 160 * 1024, "gfx950 LDS is 160 KiB per workgroup");
 
-  struct Staging {
-    u32x4 k[kNC];
-    u32x4 v[kNC];
-  };
+  using Regs = u32x4[kNC];
 
-  // Global loads of the K/V tile starting at key k0 into registers: thread tid takes 16-byte
-  // chunks tid, tid + kThreads, ... (16 consecutive threads read one whole 256-byte row at D=128).
+  // Global loads of one tensor's tile starting at key k0 into registers: thread tid takes 16-byte
+  // chunks tid, tid + kThreads, ... (16 consecutive threads read one 256-byte row at D = 128).
   // Rows past the last key (a partial last tile) are clamped to row N-1: every address stays in
   // the tensor, and those rows sit in 32-key blocks that the math skips.
-  __device__ static void load_tile(Staging& st, const T* kb, const T* vb, int k0, int N, int tid) {
+  __device__ static void load(Regs& r, const T* base, int k0, int N, int tid) {
     const int last = N - 1 - k0;
 #pragma unroll
     for (int i = 0; i < kNC; ++i) {
       const int c = tid + i * kThreads;
       if ((kChunks % kThreads == 0) || c < kChunks) {
         const int row = min(c / kRowChunks, last);
-        const size_t off = static_cast<size_t>(k0 + row) * D + (c % kRowChunks) * 8;
-        st.k[i] = *reinterpret_cast<const u32x4*>(kb + off);
-        st.v[i] = *reinterpret_cast<const u32x4*>(vb + off);
+        r[i] = *reinterpret_cast<const u32x4*>(base + static_cast<size_t>(k0 + row) * D +
+                                               (c % kRowChunks) * 8);
       }
     }
   }
 
-  __device__ static void store_tile(const Staging& st, T* buf, int tid) {
-    T* Ks = buf;
-    T* Vs = buf + kKElems;
+  template <int LD>
+  __device__ static void store(const Regs& r, T* buf, int tid) {
 #pragma unroll
     for (int i = 0; i < kNC; ++i) {
       const int c = tid + i * kThreads;
       if ((kChunks % kThreads == 0) || c < kChunks) {
-        const int row = c / kRowChunks;
-        const int col = (c % kRowChunks) * 8;
-        *reinterpret_cast<u32x4*>(Ks + row * kLdK + col) = st.k[i];
-        *reinterpret_cast<u32x4*>(Vs + row * kLdV + col) = st.v[i];
+        *reinterpret_cast<u32x4*>(buf + (c / kRowChunks) * LD + (c % kRowChunks) * 8) = r[i];
       }
     }
   }
@@ -197,122 +191,219 @@ struct Fa16 {
   struct WaveState {
     u32x4 q[D / 16];  // B operand of S^T: row n = l%32, head-dim 16*st + 8*(l/32) .. +7
     f32x16 o[kDB];    // O^T accumulator: head-dim rows, query-row columns
-    float m;          // running row max (raw score units); may lag the true max (lazy)
+    float m;          // reference max of the row (raw score units); p = exp2(s c - m c)
     float mc;         // m * c, with 0 while m == -inf
     float l;          // this lane's partial row sum relative to m (the lane pair l, l^32 adds up)
   };
 
-  // One tile for one wave: keys [kbase, kbase + 32*nvalid) of the tile take part; `diag` is the
-  // index of the 32-key block on the causal diagonal (-1 if none). vt_lane is the lane's fixed
-  // offset of the transpose read (row 4*(l/32) + (l%16)/4, column 16*((l/16)%2) + 4*(l%4)).
-  __device__ static void compute_tile(WaveState& ws, const T* buf, int kbase, int nvalid,
-                                      int diag, float c, float lazy_raw, int lane, int vt_lane) {
-    const T* Ks = buf + kbase * kLdK;
-    const T* Vs = buf + kKElems + kbase * kLdV + vt_lane;
-    const int g = lane >> 5;
-    const int r32 = lane & 31;
-    f32x16 s[kKB];
-    // ---- S^T = K Q^T ----------------------------------------------------------------------------
+  // Probabilities of one tile as MFMA operands: p[kb][h] covers keys 16h..16h+15 of block kb;
+  // plo holds the bf16 low parts of the causal diagonal block.
+  struct Probs {
+    u32x4 p[kKB][2];
+    u32x4 plo[2];
+  };
+
+  // S^T = K Q^T for the valid 32-key blocks (all of them when FULL). Ks points at the wave's keys.
+  template <bool FULL>
+  __device__ static void qk(f32x16 (&s)[kKB], const WaveState& ws, const T* Ks, int nvalid,
+                            int lane) {
+    const T* krow = Ks + (lane & 31) * kLdK + 8 * (lane >> 5);
 #pragma unroll
     for (int kb = 0; kb < kKB; ++kb) {
-      if (kb < nvalid) {
+      if (FULL || kb < nvalid) {
         f32x16 acc = {};
-        const T* krow = Ks + (32 * kb + r32) * kLdK + 8 * g;
 #pragma unroll
         for (int st = 0; st < D / 16; ++st) {
-          acc = mma<T>(*reinterpret_cast<const u32x4*>(krow + 16 * st), ws.q[st], acc);
+          acc = mma<T>(*reinterpret_cast<const u32x4*>(krow + 32 * kb * kLdK + 16 * st), ws.q[st],
+                       acc);
         }
         s[kb] = acc;
       }
     }
-    // ---- causal diagonal block: key 8(r/4) + 4g + r%4 > row r32 is masked --------------------
-    if (diag >= 0) {
-#pragma unroll
-      for (int kb = 0; kb < kKB; ++kb) {
-        if (kb == diag) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            if (8 * (r >> 2) + 4 * g + (r & 3) > r32) s[kb][r] = -__builtin_inff();
-          }
-        }
-      }
-    }
-    // ---- online softmax with lazy rescaling ----------------------------------------------------
+  }
+
+  template <bool FULL>
+  __device__ static float tile_max(const f32x16 (&s)[kKB], int nvalid) {
     float mx = -__builtin_inff();
 #pragma unroll
     for (int kb = 0; kb < kKB; ++kb) {
-      if (kb < nvalid) {
+      if (FULL || kb < nvalid) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
       }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    // The running max moves only when some row of the wave sees a score more than lazy_log2
-    // (exp2 units) above its current m; otherwise p = exp2(s c - m c) <= 2^lazy_log2 and nothing
-    // is rescaled. acc, l and lse all refer to the same m, so the result is unchanged. One ballot
-    // per tile: a skipped rescale is a scalar branch.
-    if (__builtin_amdgcn_ballot_w64(mx > ws.m + lazy_raw) != 0) {
-      const float m_new = fmaxf(ws.m, mx);
-      // A row with no visible key so far keeps m = -inf; 0 in the exponent keeps every masked
-      // p = exp2(-inf) = 0 and alpha = 0 (acc and l are still 0), never NaN.
-      const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
-      const float alpha = exp2_hw((ws.m - m_use) * c);
-      ws.l *= alpha;
+    return fmaxf(mx, __shfl_xor(mx, 32));
+  }
+
+  // Moves the reference max to max(m, mx) and rescales l and O by alpha = exp2((m_old - m_new) c).
+  __device__ static void rescale(WaveState& ws, float mx, float c) {
+    const float m_new = fmaxf(ws.m, mx);
+    // A row with no visible key so far keeps m = -inf; 0 in the exponent keeps every masked
+    // p = exp2(-inf) = 0 and alpha = 0 (acc and l are still 0), never NaN.
+    const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
+    const float alpha = exp2_hw((ws.m - m_use) * c);
+    ws.l *= alpha;
 #pragma unroll
-      for (int db = 0; db < kDB; ++db) ws.o[db] *= alpha;
-      ws.m = m_new;
-      ws.mc = m_use * c;
-    }
-#pragma unroll
-    for (int kb = 0; kb < kKB; ++kb) {
-      if (kb < nvalid) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[kb][r] = exp2_hw(__builtin_fmaf(s[kb][r], c, -ws.mc));
-      }
-    }
-    // ---- O^T += V^T P^T and the row sum ----------------------------------------------------------
+    for (int db = 0; db < kDB; ++db) ws.o[db] *= alpha;
+    ws.m = m_new;
+    ws.mc = m_use * c;
+  }
+
+  // p = exp2(s c - m c) for the valid blocks, packed into P. Returns this lane's share of the
+  // tile's row sum: over the fp16-rounded values (two per packed dot2) for fp16, so numerator and
+  // denominator use the same weights; in fp32 for bf16, whose 8 significant bits would cost the
+  // LSE its 1e-3. For bf16 the causal diagonal block also gets its low parts (P = hi + lo, exact
+  // to ~2^-16): the first rows of a sequence have all of their few keys in that block.
+  template <bool FULL>
+  __device__ static float exp_pack(const f32x16 (&s)[kKB], Probs& P, const WaveState& ws,
+                                   int nvalid, int diag, float c) {
     float rs = 0.f;
 #pragma unroll
     for (int kb = 0; kb < kKB; ++kb) {
-      if (kb < nvalid) {
+      if (FULL || kb < nvalid) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           float p[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) p[i] = s[kb][8 * h + i];
-          const u32x4 pf = pack8<T>(p);
-          u32x4 a[kDB];
-#pragma unroll
-          for (int db = 0; db < kDB; ++db) {
-            const T* vp = Vs + (32 * kb + 16 * h) * kLdV + 32 * db;
-            const u32x2 lo = lds_read_tr(vp);
-            const u32x2 hi = lds_read_tr(vp + 8 * kLdV);
-            a[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-            ws.o[db] = mma<T>(a[db], pf, ws.o[db]);
-          }
-          if constexpr (__is_same(T, _Float16)) {
-            // fp16: the row sum is taken over the probabilities exactly as they enter the
-            // product (rounded to fp16), two per packed dot2.
-            rs = dot2_ones_f16(pf, rs);
+          for (int i = 0; i < 8; ++i) p[i] = exp2_hw(__builtin_fmaf(s[kb][8 * h + i], c, -ws.mc));
+          P.p[kb][h] = pack8<T>(p);
+          if constexpr (kF16) {
+            rs = dot2_ones_f16(P.p[kb][h], rs);
           } else {
-            // bf16 keeps 8 significant bits: the row sum stays in fp32 (the LSE must hold 1e-3),
-            // and on the causal diagonal block -- where the first rows of a sequence have all of
-            // their few keys -- P is applied as hi + lo (two bf16 operands, exact to ~2^-16).
 #pragma unroll
             for (int i = 0; i < 8; ++i) rs += p[i];
-            if (kb == diag) {
+            if (!FULL && kb == diag) {
               float lo[8];
 #pragma unroll
               for (int i = 0; i < 8; ++i) lo[i] = p[i] - static_cast<float>(static_cast<__bf16>(p[i]));
-              const u32x4 pl = pack8<T>(lo);
-#pragma unroll
-              for (int db = 0; db < kDB; ++db) ws.o[db] = mma<T>(a[db], pl, ws.o[db]);
+              P.plo[h] = pack8<T>(lo);
             }
           }
         }
       }
     }
+    return rs;
+  }
+
+  // Online softmax of one tile (ref:include/fa/softmax_math.cuh:25-71), in two halves.
+  // softmax_exp masks the causal diagonal block and exponentiates against the current reference
+  // max m; softmax_settle then settles m:
+  //   fp16 -- lazy: m stays as long as every probability of the tile is <= 2^14 (the lane's tile
+  //           sum bounds each of its probabilities, and fp16 holds 65504) and the row has a
+  //           reference; otherwise the wave takes the tile max, rescales and redoes the tile;
+  //   bf16 -- exact: m is the running max, so the largest probability is exactly 1.0 (a rounded
+  //           largest probability would dominate the error of concentrated rows).
+  // acc, l and lse all refer to the same m and m only moves to an observed max, so the result is
+  // the reference's recurrence. The decision is one ballot (a scalar branch).
+  template <bool FULL>
+  __device__ static float softmax_exp(WaveState& ws, f32x16 (&s)[kKB], Probs& P, float& mx,
+                                      int nvalid, int diag, float c, int lane) {
+    if (!FULL && diag >= 0) {
+      const int g = lane >> 5;
+#pragma unroll
+      for (int kb = 0; kb < kKB; ++kb) {
+        if (kb == diag) {
+          // A select, not a conditional store: conditional element stores keep the score
+          // registers in scratch memory.
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            s[kb][r] = (8 * (r >> 2) + 4 * g + (r & 3) > (lane & 31)) ? -__builtin_inff() : s[kb][r];
+          }
+        }
+      }
+    }
+    if constexpr (!kF16) mx = tile_max<FULL>(s, nvalid);
+    return exp_pack<FULL>(s, P, ws, nvalid, diag, c);
+  }
+
+  template <bool FULL>
+  __device__ static void softmax_settle(WaveState& ws, const f32x16 (&s)[kKB], Probs& P, float rs,
+                                        float mx, int nvalid, int diag, float c) {
+    bool redo;
+    if constexpr (kF16) {
+      redo = !(rs <= kF16SumLimit) || ws.m == -__builtin_inff();
+    } else {
+      redo = mx > ws.m;
+    }
+    if (__builtin_amdgcn_ballot_w64(redo) != 0) {
+      if constexpr (kF16) mx = tile_max<FULL>(s, nvalid);
+      rescale(ws, mx, c);
+      rs = exp_pack<FULL>(s, P, ws, nvalid, diag, c);
+    }
     ws.l += rs;
+  }
+
+  // V^T operands of one tile: va[kb][h][db] covers keys 32kb + 16h .. +15 and head-dim block db.
+  // Vs points at the wave's keys plus the lane's transpose-read offset.
+  using VOps = u32x4[kKB][2][kDB];
+  __device__ static u32x4 v_operand(const T* Vs, int kb, int h, int db) {
+    const T* vp = Vs + (32 * kb + 16 * h) * kLdV + 32 * db;
+    const u32x2 lo = lds_read_tr(vp);
+    const u32x2 hi = lds_read_tr(vp + 8 * kLdV);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  }
+
+  // O^T += V^T P^T (operands read here; the partial-tile path).
+  template <bool FULL>
+  __device__ static void pv(WaveState& ws, const Probs& P, const T* Vs, int nvalid, int diag) {
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) {
+      if (FULL || kb < nvalid) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int db = 0; db < kDB; ++db) {
+            const u32x4 a = v_operand(Vs, kb, h, db);
+            ws.o[db] = mma<T>(a, P.p[kb][h], ws.o[db]);
+            if constexpr (!kF16) {
+              if (!FULL && kb == diag) ws.o[db] = mma<T>(a, P.plo[h], ws.o[db]);
+            }
+          }
+        }
+      }
+    }
+  }
+
+  // The steady-state step on full tiles: S(t+1) = K(t+1) Q^T on MFMA, interleaved with the
+  // exponentials of S(t); every LDS read of the step (K rows of t+1 and the V^T operands of t) is
+  // issued up front so that no MFMA waits on LDS latency; then the P(t) V(t) MFMAs.
+  __device__ static void step_full(WaveState& ws, f32x16 (&s_cur)[kKB], f32x16 (&s_nxt)[kKB],
+                                   Probs& P, const T* Kn, const T* Vc, float c, int lane) {
+    VOps va;
+    qk<true>(s_nxt, ws, Kn, kKB, lane);
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int db = 0; db < kDB; ++db) va[kb][h][db] = v_operand(Vc, kb, h, db);
+      }
+    }
+    float mx = 0.f;
+    const float rs = softmax_exp<true>(ws, s_cur, P, mx, kKB, -1, c, lane);
+    // Issue order for the region: the K reads, then the V^T reads, then one MFMA of S(t+1) per
+    // group of VALU ops. While an MFMA runs in the matrix core the wave keeps issuing independent
+    // VALU work (issue is in order, so a cluster of MFMAs would stall it).
+    constexpr int kMfma = kKB * (D / 16);
+    constexpr int kVReads = kKB * 2 * kDB * 2;
+    constexpr int kValu = (kF16 ? 48 : 66) * kKB;
+    constexpr int kPer = (kValu + kMfma - 1) / kMfma;
+    __builtin_amdgcn_sched_group_barrier(0x100, kMfma, 0);    // DS reads: K rows
+    __builtin_amdgcn_sched_group_barrier(0x100, kVReads, 0);  // DS reads: V^T operands
+#pragma unroll
+    for (int i = 0; i < kMfma; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x002, kPer, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);     // MFMA
+    }
+    softmax_settle<true>(ws, s_cur, P, rs, mx, kKB, -1, c);
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int db = 0; db < kDB; ++db) ws.o[db] = mma<T>(va[kb][h][db], P.p[kb][h], ws.o[db]);
+      }
+    }
   }
 
   __device__ static void run(const KArgs& a) {
@@ -345,8 +436,8 @@ struct Fa16 {
     const size_t q_off = (static_cast<size_t>(b) * a.H + h) * static_cast<size_t>(N) * D;
     const size_t kv_off = (static_cast<size_t>(b) * a.Hkv + hk) * static_cast<size_t>(N) * D;
     const T* qb = static_cast<const T*>(a.q) + q_off;
-    const T* kb = static_cast<const T*>(a.k) + kv_off;
-    const T* vb = static_cast<const T*>(a.v) + kv_off;
+    const T* kg = static_cast<const T*>(a.k) + kv_off;
+    const T* vg = static_cast<const T*>(a.v) + kv_off;
 
     const int i0 = qt * kBr;
     const int r0 = i0 + 32 * rg;  // this wave's first row
@@ -356,6 +447,8 @@ struct Fa16 {
     const int kv_end = a.causal ? min(N, i0 + kBr) : N;
     const int n_tiles = (kv_end + BC - 1) / BC;
     const int wave_end = wave_valid ? (a.causal ? min(N, r0 + 32) : N) : 0;
+    const int kbase = ks * BCW;  // this wave's keys inside every tile
+    const float c = a.c;
 
     WaveState ws;
 #pragma unroll
@@ -370,40 +463,120 @@ struct Fa16 {
     ws.mc = 0.f;
     ws.l = 0.f;
 
+    // Buffers: K[kBufs] then V[kBufs]; the wave's view starts at its key split.
+    T* const kbuf0 = lds;
+    T* const vbuf0 = lds + kBufs * kKElems;
     const int vt_lane = (4 * g + ((lane & 15) >> 2)) * kLdV + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    const float lazy_raw = lazy_log2<T>() / a.c;
-    const int kbase = ks * BCW;  // this wave's keys inside every tile
+    auto kwave = [&](int buf) -> const T* { return kbuf0 + buf * kKElems + kbase * kLdK; };
+    auto vwave = [&](int buf) -> const T* {
+      return vbuf0 + buf * kVElems + kbase * kLdV + vt_lane;
+    };
+    // Valid 32-key blocks of tile t for this wave, and its causal diagonal block (-1 if none).
+    auto nvalid_of = [&](int t) -> int {
+      return max(0, min(kKB, (wave_end - (t * BC + kbase) + 31) / 32));
+    };
+    auto diag_of = [&](int t, int nv) -> int {
+      const int d = a.causal ? (r0 - (t * BC + kbase)) / 32 : -1;  // multiples of 32
+      return (d >= 0 && d < nv) ? d : -1;
+    };
 
-    Staging st;
-    if constexpr (PREFETCH) {
-      load_tile(st, kb, vb, 0, N, tid);
-      store_tile(st, lds, tid);
+    Regs rk, rv;
+    Probs P;
+    if constexpr (PIPE) {
+      // Software pipeline: iteration t exponentiates tile t while the MFMAs of S(t+1) = K(t+1) Q^T
+      // run, then applies P(t) to V(t). K is therefore staged one tile ahead of V: iteration t
+      // reads K buffer (t+1)%2 and V buffer t%2 and refills K buffer t%2 with K(t+2) and V buffer
+      // (t+1)%2 with V(t+1), each loaded into registers at the top of the iteration.
+      {
+        // K(0), V(0) and K(1) in flight together (one memory round trip for the prologue).
+        Regs rk1;
+        load(rk, kg, 0, N, tid);
+        load(rv, vg, 0, N, tid);
+        if (n_tiles > 1) load(rk1, kg, BC, N, tid);
+        store<kLdK>(rk, kbuf0, tid);
+        store<kLdV>(rv, vbuf0, tid);
+        if (n_tiles > 1) store<kLdK>(rk1, kbuf0 + kKElems, tid);
+      }
       __syncthreads();
-      for (int t = 0; t < n_tiles; ++t) {
-        const int k0 = t * BC;
-        if (t + 1 < n_tiles) load_tile(st, kb, vb, k0 + BC, N, tid);
-        const int kw = k0 + kbase;
-        const int nvalid = max(0, min(kKB, (wave_end - kw + 31) / 32));
-        if (nvalid > 0) {
-          const int diag = a.causal ? (r0 - kw) / 32 : -1;  // r0, kw multiples of 32
-          compute_tile(ws, lds + (t & 1) * kBufElems, kbase, nvalid,
-                       (diag >= 0 && diag < nvalid) ? diag : -1, a.c, lazy_raw, lane, vt_lane);
+      f32x16 sa[kKB], sb[kKB];
+      {
+        const int nv0 = nvalid_of(0);
+        if (nv0 > 0) qk<false>(sa, ws, kwave(0), nv0, lane);
+      }
+      __syncthreads();  // K buffer 0 is refilled in iteration 0
+      // One pipeline step. `full` (a compile-time tag) selects the steady-state body: tiles t and
+      // t+1 are full for every wave of the workgroup and carry no causal diagonal, so the body has
+      // no per-block branches and the VALU softmax of S(t) interleaves with the MFMAs of S(t+1).
+      // The parity tag makes the calls with swapped S arrays distinct instantiations (one function
+      // called with swapped arrays gets its calls merged through pointer phis, which pins the
+      // arrays in scratch memory).
+      auto iter = [&](auto full, auto parity, int t, f32x16(&s_cur)[kKB],
+                      f32x16(&s_nxt)[kKB]) __attribute__((always_inline)) {
+        (void)parity;
+        constexpr bool kFull = decltype(full)::value;
+        if (t + 2 < n_tiles) load(rk, kg, (t + 2) * BC, N, tid);
+        if (t + 1 < n_tiles) load(rv, vg, (t + 1) * BC, N, tid);
+        const T* kn = kwave((t + 1) & 1);
+        const T* vc = vwave(t & 1);
+        if constexpr (kFull) {
+          step_full(ws, s_cur, s_nxt, P, kn, vc, c, lane);
+        } else {
+          const int nv = nvalid_of(t);
+          const int dg = diag_of(t, nv);
+          const int nv_nxt = (t + 1 < n_tiles) ? nvalid_of(t + 1) : 0;
+          if (nv_nxt > 0) qk<false>(s_nxt, ws, kn, nv_nxt, lane);
+          if (nv > 0) {
+            float mx = 0.f;
+            const float rs = softmax_exp<false>(ws, s_cur, P, mx, nv, dg, c, lane);
+            softmax_settle<false>(ws, s_cur, P, rs, mx, nv, dg, c);
+            pv<false>(ws, P, vc, nv, dg);
+          }
         }
-        if (t + 1 < n_tiles) store_tile(st, lds + ((t + 1) & 1) * kBufElems, tid);
+        if (t + 2 < n_tiles) store<kLdK>(rk, kbuf0 + (t & 1) * kKElems, tid);
+        if (t + 1 < n_tiles) store<kLdV>(rv, vbuf0 + ((t + 1) & 1) * kVElems, tid);
         __syncthreads();
+      };
+      using Full = std::true_type;
+      using Part = std::false_type;
+      using P0 = std::integral_constant<int, 0>;
+      using P1 = std::integral_constant<int, 1>;
+      // Tiles [0, n_full) are full for every wave and carry no diagonal (workgroup-uniform): key
+      // tile t is complete below the workgroup's first row (causal) or below N.
+      const int n_full = (a.causal ? i0 : N) / BC;
+      const int n_steady = max(0, min(n_tiles, n_full) - 1);
+      // Unrolled by two so the S(t) / S(t+1) register sets swap roles without copies; the steady
+      // loop and the tail loop get independent register assignments.
+      int t = 0;
+      for (; t + 1 < n_steady; t += 2) {
+        iter(Full{}, P0{}, t, sa, sb);
+        iter(Full{}, P1{}, t + 1, sb, sa);
+      }
+      if (t < n_steady) {
+        iter(Full{}, P0{}, t, sa, sb);
+        ++t;
+        if (t < n_tiles) iter(Part{}, P1{}, t, sb, sa);
+        ++t;
+      }
+      for (; t < n_tiles; t += 2) {
+        iter(Part{}, P0{}, t, sa, sb);
+        if (t + 1 < n_tiles) iter(Part{}, P1{}, t + 1, sb, sa);
       }
     } else {
+      f32x16 s[kKB];
       for (int t = 0; t < n_tiles; ++t) {
-        const int k0 = t * BC;
-        load_tile(st, kb, vb, k0, N, tid);
-        store_tile(st, lds, tid);
+        load(rk, kg, t * BC, N, tid);
+        load(rv, vg, t * BC, N, tid);
+        store<kLdK>(rk, kbuf0, tid);
+        store<kLdV>(rv, vbuf0, tid);
         __syncthreads();
-        const int kw = k0 + kbase;
-        const int nvalid = max(0, min(kKB, (wave_end - kw + 31) / 32));
-        if (nvalid > 0) {
-          const int diag = a.causal ? (r0 - kw) / 32 : -1;
-          compute_tile(ws, lds, kbase, nvalid, (diag >= 0 && diag < nvalid) ? diag : -1, a.c,
-                       lazy_raw, lane, vt_lane);
+        const int nv = nvalid_of(t);
+        if (nv > 0) {
+          const int dg = diag_of(t, nv);
+          qk<false>(s, ws, kwave(0), nv, lane);
+          float mx = 0.f;
+          const float rs = softmax_exp<false>(ws, s, P, mx, nv, dg, c, lane);
+          softmax_settle<false>(ws, s, P, rs, mx, nv, dg, c);
+          pv<false>(ws, P, vwave(0), nv, dg);
         }
         __syncthreads();
       }
@@ -425,14 +598,14 @@ struct Fa16 {
       __syncthreads();
       if (ks > 0) return;
 #pragma unroll
-      for (int s = 1; s < KS; ++s) {
-        const float* src = mg + ((s - 1) * RG + rg) * kMergeFloats;
+      for (int sp = 1; sp < KS; ++sp) {
+        const float* src = mg + ((sp - 1) * RG + rg) * kMergeFloats;
         const float m1 = src[kDB * 16 * 64 + lane];
         const float l1 = src[(kDB * 16 + 1) * 64 + lane];
         const float m_new = fmaxf(ws.m, m1);
         const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
-        const float a0 = exp2_hw((ws.m - m_use) * a.c);
-        const float a1 = exp2_hw((m1 - m_use) * a.c);
+        const float a0 = exp2_hw((ws.m - m_use) * c);
+        const float a1 = exp2_hw((m1 - m_use) * c);
         ws.l = ws.l * a0 + l1 * a1;
 #pragma unroll
         for (int db = 0; db < kDB; ++db) {
@@ -457,7 +630,7 @@ struct Fa16 {
         const int d = 32 * db + 8 * j + 4 * g;
         const float x0 = ws.o[db][4 * j + 0] * inv, x1 = ws.o[db][4 * j + 1] * inv;
         const float x2 = ws.o[db][4 * j + 2] * inv, x3 = ws.o[db][4 * j + 3] * inv;
-        if constexpr (__is_same(T, _Float16)) {
+        if constexpr (kF16) {
           *reinterpret_cast<f16x4*>(orow + d) =
               f16x4{(_Float16)x0, (_Float16)x1, (_Float16)x2, (_Float16)x3};
         } else {
@@ -508,37 +681,37 @@ constexpr Variant variant() {
 
 // ---- instantiation tables: one (RG, KS, BCW) per (BR, BC) -------------------------------------
 // Stage 5 rows cover the default tiles, the sweep set and the tile-invariance set, including
-// key-split variants at every height so the merge path is tested at small N.
+// key-split variants at every height so the merge path is tested at small N. Every row fits the
+// register budget of its occupancy without spills (256 VGPRs per wave at 8 waves per workgroup);
+// that is what rules out BCW = 64 at D = 128 with 8 waves and BR 256 / BC 128.
 template <typename T, int D>
 struct S5Rows {
   static constexpr Variant rows[] = {
-      variant<5, T, D, 1, 1, 32>(),   // BR  32, BC  32
-      variant<5, T, D, 1, 2, 32>(),   // BR  32, BC  64 (2-way split)
-      variant<5, T, D, 2, 1, 32>(),   // BR  64, BC  32
-      variant<5, T, D, 2, 2, 32>(),   // BR  64, BC  64 (2-way split)
-      variant<5, T, D, 2, 2, 64>(),   // BR  64, BC 128 (2-way split)
-      variant<5, T, D, 4, 1, 32>(),   // BR 128, BC  32
-      variant<5, T, D, 4, 2, 32>(),   // BR 128, BC  64 (2-way split)
-      variant<5, T, D, 4, 2, 64>(),   // BR 128, BC 128 (2-way split) -- default
-      variant<5, T, D, 8, 1, 64>(),   // BR 256, BC  64
-      variant<5, T, D, 8, 1, 128>(),  // BR 256, BC 128
+      variant<5, T, D, 1, 1, 32>(),  // BR  32, BC  32
+      variant<5, T, D, 1, 2, 32>(),  // BR  32, BC  64 (2-way split)
+      variant<5, T, D, 2, 1, 32>(),  // BR  64, BC  32
+      variant<5, T, D, 2, 2, 32>(),  // BR  64, BC  64 (2-way split)
+      variant<5, T, D, 2, 2, 64>(),  // BR  64, BC 128 (2-way split, 4 waves)
+      variant<5, T, D, 4, 1, 32>(),  // BR 128, BC  32
+      variant<5, T, D, 4, 2, 32>(),  // BR 128, BC  64 (2-way split) -- D = 128 default
+      variant<5, T, D, 8, 1, 64>(),  // BR 256, BC  64
   };
 };
 
+// BR 128 / BC 128 (4 row groups x 2 key splits of 64 keys, the D = 64 default) at D = 64 only.
 template <typename T>
 VariantList s5_table() {
   static const Variant t[] = {
       S5Rows<T, 64>::rows[0],  S5Rows<T, 64>::rows[1],  S5Rows<T, 64>::rows[2],
       S5Rows<T, 64>::rows[3],  S5Rows<T, 64>::rows[4],  S5Rows<T, 64>::rows[5],
-      S5Rows<T, 64>::rows[6],  S5Rows<T, 64>::rows[7],  S5Rows<T, 64>::rows[8],
-      S5Rows<T, 64>::rows[9],  S5Rows<T, 128>::rows[0], S5Rows<T, 128>::rows[1],
-      S5Rows<T, 128>::rows[2], S5Rows<T, 128>::rows[3], S5Rows<T, 128>::rows[4],
-      S5Rows<T, 128>::rows[5], S5Rows<T, 128>::rows[6], S5Rows<T, 128>::rows[7],
-      S5Rows<T, 128>::rows[8], S5Rows<T, 128>::rows[9]};
+      S5Rows<T, 64>::rows[6],  S5Rows<T, 64>::rows[7],  variant<5, T, 64, 4, 2, 64>(),
+      S5Rows<T, 128>::rows[0], S5Rows<T, 128>::rows[1], S5Rows<T, 128>::rows[2],
+      S5Rows<T, 128>::rows[3], S5Rows<T, 128>::rows[4], S5Rows<T, 128>::rows[5],
+      S5Rows<T, 128>::rows[6], S5Rows<T, 128>::rows[7]};
   return VariantList{t, static_cast<int>(sizeof(t) / sizeof(t[0]))};
 }
 
-// Stage 4: BR fixed at 128 (4 row groups x 2 key splits), BC in {64, 128}; BC 32 without split.
+// Stage 4: BR fixed at 128 (4 row groups), BC in {32, 64, 128}.
 template <typename T>
 VariantList s4_table() {
   static const Variant t[] = {variant<4, T, 64, 4, 1, 32>(),  variant<4, T, 64, 4, 2, 32>(),

@@ -201,10 +201,11 @@ int launch_selected(const char* tag, VariantList list, int br, int bc, const KAr
 }
 
 // Workgroup height / key tile defaults per stage (overridable by FA_FORCE_BR/BC where the
-// stage honours them). Matrix-core stages: BR = 128 rows = 4 row groups of 32, BC = 128 keys
-// split in two halves of 64 (8 waves, 2 per SIMD). fp32 rung: 4 waves of 32 rows, BC = 32.
+// stage honours them). Matrix-core stages: BR = 128 rows = 4 row groups of 32 and two key splits
+// (8 waves, 2 per SIMD); each wave takes 64 keys of every tile at D = 64 (BC = 128) and 32 at
+// D = 128 (BC = 64), the widest that fits 256 VGPRs. fp32 rung: 4 waves of 32 rows, BC = 32.
 constexpr int kDefaultBr = 128;
-constexpr int kDefaultBcMfma = 128;
+constexpr int default_bc_mfma(int D) { return D == 64 ? 128 : 64; }
 constexpr int kDefaultBcF32 = 32;
 
 }  // namespace
@@ -223,7 +224,7 @@ int forward(int dtype, const void* q, const void* k, const void* v, void* o, flo
   const int rc = common_stage_checks("stage5", q, k, v, o, lse, p);
   if (rc != 0) return rc;
   const int br = dbg.block_m != 0 ? dbg.block_m : kDefaultBr;
-  const int bc = dbg.block_n != 0 ? dbg.block_n : kDefaultBcMfma;
+  const int bc = dbg.block_n != 0 ? dbg.block_n : default_bc_mfma(p.D);
   const KArgs a = make_args(q, k, v, o, lse, p);
   const VariantList list = dtype == FA_DTYPE_F16 ? variants_s5_f16() : variants_s5_bf16();
   return launch_selected("stage5", list, br, bc, a, p.D, stream);
@@ -245,7 +246,7 @@ int forward(int dtype, const void* q, const void* k, const void* v, void* o, flo
     std::fprintf(stderr, "fa::stage4: FA_FORCE_BR=%d ignored (BR is fixed at %d)\n", dbg.block_m,
                  kDefaultBr);
   }
-  const int bc = dbg.block_n != 0 ? dbg.block_n : kDefaultBcMfma;
+  const int bc = dbg.block_n != 0 ? dbg.block_n : default_bc_mfma(p.D);
   const KArgs a = make_args(q, k, v, o, lse, p);
   const VariantList list = dtype == FA_DTYPE_F16 ? variants_s4_f16() : variants_s4_bf16();
   return launch_selected("stage4", list, kDefaultBr, bc, a, p.D, stream);

@@ -31,8 +31,8 @@ STAGE_DTYPE_PAIRS = [(s, dt) for s in (3, 4, 5) for dt in STAGE_DTYPES[s]]
 # 0 = default). Stages 3 and 4 fix BR at 128 and ignore a forced BR, as the reference's S3/S4 do.
 STAGE_BC = {3: {32, 64}, 4: {32, 64, 128}}
 S5_TILES = {(32, 32), (32, 64), (64, 32), (64, 64), (64, 128), (128, 32), (128, 64), (128, 128),
-            (256, 64), (256, 128)}
-S5_DEFAULT = (128, 128)
+            (256, 64)}
+S5_DEFAULT = (128, 128)  # at D = 64, the head dim of the tile tests
 
 _ids = {torch.float32: "fp32", torch.float16: "fp16", torch.bfloat16: "bf16"}
 
