@@ -286,8 +286,10 @@ def main(argv=None) -> int:
         for name in WORKLOADS:
             if name == a.workload:
                 continue
-            res, s2, _, _, _ = bench_workload(torch, capi, name, 5, max(20, a.steps // 4),
-                                              a.warmup)
+            # Each secondary config gets its own long warm-up: it follows a different workload
+            # (and the CPU baseline's idle GPU), and the clock settles within tens of launches.
+            res, s2, _, _, _ = bench_workload(torch, capi, name, 5, max(50, a.steps // 2),
+                                              max(50, a.warmup))
             del s2
             others[name] = {kk: (round(vv, 6) if isinstance(vv, float) else vv)
                             for kk, vv in res.items()}

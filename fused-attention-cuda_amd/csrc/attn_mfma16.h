@@ -38,10 +38,11 @@
 //                 (16h + 8c + 4g + j, c = 0..1, g = l/32) that the probability registers of lane l
 //                 hold. P never leaves registers and no VALU transposition is needed.
 //
-// LDS layout per buffer: Ks[BC][D + 8] then Vs[BC][D + 16] (16-bit elements). The K pad (16 B)
-// puts the 8 rows read by 8 consecutive lanes on 8 distinct 16-byte bank groups; the V pad (32 B)
-// puts the 4 rows of a 16-lane transpose read on 4 distinct 32-byte bank groups. Tile stores are
-// whole 16-byte row segments (conflict-free).
+// LDS layout: K and V tiles are BC rows of D 16-bit elements, unpadded, with the 16-byte chunks
+// of each row XOR-swizzled (K by row & 7, V by 2 (row & 3)) so that the 8 rows of one K operand
+// read and the 4 rows of one V transpose read hit distinct banks. Tiles are written straight
+// from HBM by global_load_lds_dwordx4 (no register staging), one contiguous KiB per wave
+// instruction; the swizzle is applied on the global side by choosing each lane's source chunk.
 //
 // Grid: 1-D, (ceil(N/BR) * B * H) workgroups. Hardware hands workgroup i to XCD i % 8 (each XCD
 // has its own L2); blockIdx is remapped so that each XCD receives a contiguous range of
@@ -132,17 +133,16 @@ struct Fa16 {
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int kBr = 32 * RG;
   static constexpr int BC = KS * BCW;
-  static constexpr int kLdK = D + 8;   // K row stride (elements)
-  static constexpr int kLdV = D + 16;  // V row stride (elements)
-  static constexpr int kKElems = BC * kLdK;  // one K buffer
-  static constexpr int kVElems = BC * kLdV;  // one V buffer
+  static constexpr int kKElems = BC * D;  // one K buffer (unpadded rows, swizzled chunks)
+  static constexpr int kVElems = BC * D;  // one V buffer
   static constexpr int kBufs = PIPE ? 2 : 1;
   static constexpr size_t kTileBytes = static_cast<size_t>(kBufs) * (kKElems + kVElems) * 2;
   static constexpr int kKB = BCW / 32;  // 32-key blocks per wave and tile
   static constexpr int kDB = D / 32;    // 32-wide head-dim blocks of O^T
   static constexpr int kRowChunks = D / 8;         // 16-byte chunks per K/V row
   static constexpr int kChunks = BC * kRowChunks;  // per tensor and tile
-  static constexpr int kNC = (kChunks + kThreads - 1) / kThreads;
+  static constexpr int kDmaInsts = kChunks / 64;   // 1 KiB LDS-DMA instructions per tensor/tile
+  static constexpr int kDmaPerWave = kDmaInsts / kWaves;
   // Merge scratch: every non-leading key split writes its O^T registers, m and l per lane.
   static constexpr int kMergeFloats = (kDB * 16 + 2) * 64;
   static constexpr size_t kMergeBytes =
@@ -157,36 +157,67 @@ struct Fa16 {
   static_assert(D == 64 || D == 128, "D must be 64 or 128");
   static_assert(kWaves >= 1 && kWaves <= 16, "1..16 waves");
   static_assert(kLdsBytes <= 160 * 1024, "gfx950 LDS is 160 KiB per workgroup");
+  static_assert(kChunks % 64 == 0, "a tile is a whole number of 1 KiB DMA instructions");
+  static_assert(kDmaInsts % kWaves == 0, "every wave issues the same number of DMA instructions");
 
-  using Regs = u32x4[kNC];
+  // LDS layout of a K/V tile: BC rows of D elements, unpadded; the 16-byte chunk c of row r
+  // lives at chunk position c ^ swz(r). K uses swz(r) = r & 7: the 8 rows that 8 consecutive
+  // lanes read for one MFMA operand land on 8 distinct 16-byte bank groups. V uses
+  // swz(r) = 2 (r & 3): the 4 rows of one 16-lane transpose read land their 32-byte segments on
+  // 4 distinct bank ranges.
+  template <bool IS_V>
+  __device__ static int swz(int row) {
+    return IS_V ? 2 * (row & 3) : (row & 7);
+  }
 
-  // Global loads of one tensor's tile starting at key k0 into registers: thread tid takes 16-byte
-  // chunks tid, tid + kThreads, ... (16 consecutive threads read one 256-byte row at D = 128).
-  // Rows past the last key (a partial last tile) are clamped to row N-1: every address stays in
-  // the tensor, and those rows sit in 32-key blocks that the math skips.
-  __device__ static void load(Regs& r, const T* base, int k0, int N, int tid) {
-    const int last = N - 1 - k0;
+  // Tiles go straight from HBM into LDS with global_load_lds_dwordx4: lane i of a wave
+  // instruction writes LDS bytes [16 i, 16 i + 16) of that instruction's 1 KiB (M0 + 16 * lane,
+  // verified on the box), so the global side picks, per lane, the chunk that belongs at that
+  // position. Instruction j of a tile goes to wave j % kWaves. Dma holds a lane's source for each
+  // of its instructions relative to the tile's first key: the tile-local row and the element
+  // offset row * D + swizzled chunk * 8 (loop-invariant).
+  struct Dma {
+    int row[kDmaPerWave];
+    int off[kDmaPerWave];
+  };
+  template <bool IS_V>
+  __device__ static Dma dma_lane(int wave, int lane) {
+    Dma d;
 #pragma unroll
-    for (int i = 0; i < kNC; ++i) {
-      const int c = tid + i * kThreads;
-      if ((kChunks % kThreads == 0) || c < kChunks) {
-        const int row = min(c / kRowChunks, last);
-        r[i] = *reinterpret_cast<const u32x4*>(base + static_cast<size_t>(k0 + row) * D +
-                                               (c % kRowChunks) * 8);
+    for (int i = 0; i < kDmaPerWave; ++i) {
+      const int pos = 64 * (wave + i * kWaves) + lane;  // chunk position in the tile
+      d.row[i] = pos / kRowChunks;
+      d.off[i] = d.row[i] * D + 8 * ((pos % kRowChunks) ^ swz<IS_V>(d.row[i]));
+    }
+    return d;
+  }
+
+  // The tile of keys [k0, k0 + BC) of one tensor into `buf`. Rows past the last key (a partial
+  // last tile) read row N-1: every address stays in the tensor, and those rows sit in 32-key
+  // blocks that the math skips. The caller waits on vmcnt before the barrier that publishes it.
+  template <bool IS_V>
+  __device__ static void dma_tile(T* buf, const T* gbase, const Dma& d, int k0, int N, int wave) {
+    const T* tile = gbase + static_cast<size_t>(k0) * D;
+    if (k0 + BC <= N) {  // workgroup-uniform
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) {
+        __builtin_amdgcn_global_load_lds(
+            (const void __attribute__((address_space(1)))*)(tile + d.off[i]),
+            (void __attribute__((address_space(3)))*)(buf + 512 * (wave + i * kWaves)), 16, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) {
+        const int last = min(d.row[i], N - 1 - k0);
+        __builtin_amdgcn_global_load_lds(
+            (const void __attribute__((address_space(1)))*)(tile + d.off[i] + (last - d.row[i]) * D),
+            (void __attribute__((address_space(3)))*)(buf + 512 * (wave + i * kWaves)), 16, 0, 0);
       }
     }
   }
 
-  template <int LD>
-  __device__ static void store(const Regs& r, T* buf, int tid) {
-#pragma unroll
-    for (int i = 0; i < kNC; ++i) {
-      const int c = tid + i * kThreads;
-      if ((kChunks % kThreads == 0) || c < kChunks) {
-        *reinterpret_cast<u32x4*>(buf + (c / kRowChunks) * LD + (c % kRowChunks) * 8) = r[i];
-      }
-    }
-  }
+  // Waits until this wave's LDS-DMA loads have landed (vmcnt(0); expcnt and lgkmcnt untouched).
+  __device__ static void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
   struct WaveState {
     u32x4 q[D / 16];  // B operand of S^T: row n = l%32, head-dim 16*st + 8*(l/32) .. +7
@@ -204,18 +235,31 @@ struct Fa16 {
   };
 
   // S^T = K Q^T for the valid 32-key blocks (all of them when FULL). Ks points at the wave's keys.
+  // Lane l reads key row l % 32 of each block, chunk 2 st + l / 32 (head-dim 16 st + 8 (l/32));
+  // the row's swizzle is l & 7 because every 32-key block starts at a multiple of 8. The lane's
+  // offsets are loop-invariant: KLane holds them.
+  struct KLane {
+    int off[D / 16];
+  };
+  __device__ static KLane k_lane(int lane) {
+    KLane k;
+#pragma unroll
+    for (int st = 0; st < D / 16; ++st) {
+      k.off[st] = (lane & 31) * D + 8 * ((2 * st + (lane >> 5)) ^ (lane & 7));
+    }
+    return k;
+  }
   template <bool FULL>
   __device__ static void qk(f32x16 (&s)[kKB], const WaveState& ws, const T* Ks, int nvalid,
-                            int lane) {
-    const T* krow = Ks + (lane & 31) * kLdK + 8 * (lane >> 5);
+                            const KLane& kl) {
 #pragma unroll
     for (int kb = 0; kb < kKB; ++kb) {
       if (FULL || kb < nvalid) {
         f32x16 acc = {};
 #pragma unroll
         for (int st = 0; st < D / 16; ++st) {
-          acc = mma<T>(*reinterpret_cast<const u32x4*>(krow + 32 * kb * kLdK + 16 * st), ws.q[st],
-                       acc);
+          const u32x4 a = *reinterpret_cast<const u32x4*>(Ks + 32 * kb * D + kl.off[st]);
+          acc = mma<T>(a, ws.q[st], acc);
         }
         s[kb] = acc;
       }
@@ -334,18 +378,35 @@ struct Fa16 {
   }
 
   // V^T operands of one tile: va[kb][h][db] covers keys 32kb + 16h .. +15 and head-dim block db.
-  // Vs points at the wave's keys plus the lane's transpose-read offset.
+  // Vs points at the wave's keys. Lane l = 16 G + 4 j + q of a transpose read addresses key
+  // row 4 (G/2) + j (+ 8 for the second read) at head-dim 32 db + 16 (G%2) + 4 q; the row's
+  // swizzle is 2 j (rows start at multiples of 4), so the lane's offset for block db is a
+  // loop-invariant per-lane constant, VLane::off[db].
   using VOps = u32x4[kKB][2][kDB];
-  __device__ static u32x4 v_operand(const T* Vs, int kb, int h, int db) {
-    const T* vp = Vs + (32 * kb + 16 * h) * kLdV + 32 * db;
+  struct VLane {
+    int off[kDB];
+  };
+  __device__ static VLane v_lane(int lane) {
+    const int G = lane >> 4, j = (lane >> 2) & 3, q = lane & 3;
+    VLane v;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) {
+      const int chunk = (4 * db + 2 * (G & 1) + (q >> 1)) ^ (2 * j);
+      v.off[db] = (4 * (G >> 1) + j) * D + 8 * chunk + 4 * (q & 1);
+    }
+    return v;
+  }
+  __device__ static u32x4 v_operand(const T* Vs, const VLane& vl, int kb, int h, int db) {
+    const T* vp = Vs + (32 * kb + 16 * h) * D + vl.off[db];
     const u32x2 lo = lds_read_tr(vp);
-    const u32x2 hi = lds_read_tr(vp + 8 * kLdV);
+    const u32x2 hi = lds_read_tr(vp + 8 * D);
     return u32x4{lo[0], lo[1], hi[0], hi[1]};
   }
 
   // O^T += V^T P^T (operands read here; the partial-tile path).
   template <bool FULL>
-  __device__ static void pv(WaveState& ws, const Probs& P, const T* Vs, int nvalid, int diag) {
+  __device__ static void pv(WaveState& ws, const Probs& P, const T* Vs, const VLane& vl, int nvalid,
+                            int diag) {
 #pragma unroll
     for (int kb = 0; kb < kKB; ++kb) {
       if (FULL || kb < nvalid) {
@@ -353,7 +414,7 @@ struct Fa16 {
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
           for (int db = 0; db < kDB; ++db) {
-            const u32x4 a = v_operand(Vs, kb, h, db);
+            const u32x4 a = v_operand(Vs, vl, kb, h, db);
             ws.o[db] = mma<T>(a, P.p[kb][h], ws.o[db]);
             if constexpr (!kF16) {
               if (!FULL && kb == diag) ws.o[db] = mma<T>(a, P.plo[h], ws.o[db]);
@@ -368,15 +429,16 @@ struct Fa16 {
   // exponentials of S(t); every LDS read of the step (K rows of t+1 and the V^T operands of t) is
   // issued up front so that no MFMA waits on LDS latency; then the P(t) V(t) MFMAs.
   __device__ static void step_full(WaveState& ws, f32x16 (&s_cur)[kKB], f32x16 (&s_nxt)[kKB],
-                                   Probs& P, const T* Kn, const T* Vc, float c, int lane) {
+                                   Probs& P, const T* Kn, const T* Vc, const KLane& kl,
+                                   const VLane& vl, float c, int lane) {
     VOps va;
-    qk<true>(s_nxt, ws, Kn, kKB, lane);
+    qk<true>(s_nxt, ws, Kn, kKB, kl);
 #pragma unroll
     for (int kb = 0; kb < kKB; ++kb) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int db = 0; db < kDB; ++db) va[kb][h][db] = v_operand(Vc, kb, h, db);
+        for (int db = 0; db < kDB; ++db) va[kb][h][db] = v_operand(Vc, vl, kb, h, db);
       }
     }
     float mx = 0.f;
@@ -466,11 +528,12 @@ struct Fa16 {
     // Buffers: K[kBufs] then V[kBufs]; the wave's view starts at its key split.
     T* const kbuf0 = lds;
     T* const vbuf0 = lds + kBufs * kKElems;
-    const int vt_lane = (4 * g + ((lane & 15) >> 2)) * kLdV + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    auto kwave = [&](int buf) -> const T* { return kbuf0 + buf * kKElems + kbase * kLdK; };
-    auto vwave = [&](int buf) -> const T* {
-      return vbuf0 + buf * kVElems + kbase * kLdV + vt_lane;
-    };
+    const KLane kl = k_lane(lane);
+    const VLane vl = v_lane(lane);
+    const Dma dk = dma_lane<false>(wave, lane);
+    const Dma dv = dma_lane<true>(wave, lane);
+    auto kwave = [&](int buf) -> const T* { return kbuf0 + buf * kKElems + kbase * D; };
+    auto vwave = [&](int buf) -> const T* { return vbuf0 + buf * kVElems + kbase * D; };
     // Valid 32-key blocks of tile t for this wave, and its causal diagonal block (-1 if none).
     auto nvalid_of = [&](int t) -> int {
       return max(0, min(kKB, (wave_end - (t * BC + kbase) + 31) / 32));
@@ -480,28 +543,22 @@ struct Fa16 {
       return (d >= 0 && d < nv) ? d : -1;
     };
 
-    Regs rk, rv;
     Probs P;
     if constexpr (PIPE) {
       // Software pipeline: iteration t exponentiates tile t while the MFMAs of S(t+1) = K(t+1) Q^T
       // run, then applies P(t) to V(t). K is therefore staged one tile ahead of V: iteration t
       // reads K buffer (t+1)%2 and V buffer t%2 and refills K buffer t%2 with K(t+2) and V buffer
       // (t+1)%2 with V(t+1), each loaded into registers at the top of the iteration.
-      {
-        // K(0), V(0) and K(1) in flight together (one memory round trip for the prologue).
-        Regs rk1;
-        load(rk, kg, 0, N, tid);
-        load(rv, vg, 0, N, tid);
-        if (n_tiles > 1) load(rk1, kg, BC, N, tid);
-        store<kLdK>(rk, kbuf0, tid);
-        store<kLdV>(rv, vbuf0, tid);
-        if (n_tiles > 1) store<kLdK>(rk1, kbuf0 + kKElems, tid);
-      }
+      // K(0), V(0) and K(1) in flight together (one memory round trip for the prologue).
+      dma_tile<false>(kbuf0, kg, dk, 0, N, wave);
+      dma_tile<true>(vbuf0, vg, dv, 0, N, wave);
+      if (n_tiles > 1) dma_tile<false>(kbuf0 + kKElems, kg, dk, BC, N, wave);
+      wait_dma();
       __syncthreads();
       f32x16 sa[kKB], sb[kKB];
       {
         const int nv0 = nvalid_of(0);
-        if (nv0 > 0) qk<false>(sa, ws, kwave(0), nv0, lane);
+        if (nv0 > 0) qk<false>(sa, ws, kwave(0), nv0, kl);
       }
       __syncthreads();  // K buffer 0 is refilled in iteration 0
       // One pipeline step. `full` (a compile-time tag) selects the steady-state body: tiles t and
@@ -514,26 +571,26 @@ struct Fa16 {
                       f32x16(&s_nxt)[kKB]) __attribute__((always_inline)) {
         (void)parity;
         constexpr bool kFull = decltype(full)::value;
-        if (t + 2 < n_tiles) load(rk, kg, (t + 2) * BC, N, tid);
-        if (t + 1 < n_tiles) load(rv, vg, (t + 1) * BC, N, tid);
+        // K(t+2) and V(t+1) go straight into the buffers this iteration does not read.
+        if (t + 2 < n_tiles) dma_tile<false>(kbuf0 + (t & 1) * kKElems, kg, dk, (t + 2) * BC, N, wave);
+        if (t + 1 < n_tiles) dma_tile<true>(vbuf0 + ((t + 1) & 1) * kVElems, vg, dv, (t + 1) * BC, N, wave);
         const T* kn = kwave((t + 1) & 1);
         const T* vc = vwave(t & 1);
         if constexpr (kFull) {
-          step_full(ws, s_cur, s_nxt, P, kn, vc, c, lane);
+          step_full(ws, s_cur, s_nxt, P, kn, vc, kl, vl, c, lane);
         } else {
           const int nv = nvalid_of(t);
           const int dg = diag_of(t, nv);
           const int nv_nxt = (t + 1 < n_tiles) ? nvalid_of(t + 1) : 0;
-          if (nv_nxt > 0) qk<false>(s_nxt, ws, kn, nv_nxt, lane);
+          if (nv_nxt > 0) qk<false>(s_nxt, ws, kn, nv_nxt, kl);
           if (nv > 0) {
             float mx = 0.f;
             const float rs = softmax_exp<false>(ws, s_cur, P, mx, nv, dg, c, lane);
             softmax_settle<false>(ws, s_cur, P, rs, mx, nv, dg, c);
-            pv<false>(ws, P, vc, nv, dg);
+            pv<false>(ws, P, vc, vl, nv, dg);
           }
         }
-        if (t + 2 < n_tiles) store<kLdK>(rk, kbuf0 + (t & 1) * kKElems, tid);
-        if (t + 1 < n_tiles) store<kLdV>(rv, vbuf0 + ((t + 1) & 1) * kVElems, tid);
+        wait_dma();
         __syncthreads();
       };
       using Full = std::true_type;
@@ -564,19 +621,18 @@ struct Fa16 {
     } else {
       f32x16 s[kKB];
       for (int t = 0; t < n_tiles; ++t) {
-        load(rk, kg, t * BC, N, tid);
-        load(rv, vg, t * BC, N, tid);
-        store<kLdK>(rk, kbuf0, tid);
-        store<kLdV>(rv, vbuf0, tid);
+        dma_tile<false>(kbuf0, kg, dk, t * BC, N, wave);
+        dma_tile<true>(vbuf0, vg, dv, t * BC, N, wave);
+        wait_dma();
         __syncthreads();
         const int nv = nvalid_of(t);
         if (nv > 0) {
           const int dg = diag_of(t, nv);
-          qk<false>(s, ws, kwave(0), nv, lane);
+          qk<false>(s, ws, kwave(0), nv, kl);
           float mx = 0.f;
           const float rs = softmax_exp<false>(ws, s, P, mx, nv, dg, c, lane);
           softmax_settle<false>(ws, s, P, rs, mx, nv, dg, c);
-          pv<false>(ws, P, vwave(0), nv, dg);
+          pv<false>(ws, P, vwave(0), vl, nv, dg);
         }
         __syncthreads();
       }
