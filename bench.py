@@ -219,6 +219,25 @@ def bench_workload(torch, capi, name, stage, steps, warmup, seed=0, gate_it=True
     return res, sets, stream, causal, scale
 
 
+def gpt_block_line(torch):
+    """one GPT-2-small decoder block (768 wide, 12 heads of 64, T 1024, batch 8,
+    fp16, causal, random init, random token ids through a wte/wpe embedding), tokens/s with the
+    attention call swapped (fused strided op / fused op after .contiguous() copies / torch SDPA);
+    warm timing as the reference's ref:bench/gpt_block.py:141-158."""
+    from fused_attn import gpt_block
+
+    idx = gpt_block.token_ids(8, 1024, seed=0)
+    out = {"config": "GPT-2-small block: n_embd 768, 12 heads (D 64), T 1024, batch 8, fp16, "
+                     "causal, random init, token ids through wte/wpe"}
+    for kind in ("fused", "fused_dense", "sdpa"):
+        model = gpt_block.build(kind, seed=0)
+        res = gpt_block.measure(model, idx, warmup=10, iters=50)
+        out[kind] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()}
+        del model
+        torch.cuda.empty_cache()
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -308,6 +327,7 @@ def main(argv=None) -> int:
             others[name] = {kk: (round(vv, 6) if isinstance(vv, float) else vv)
                             for kk, vv in res.items()}
         line["configs"] = others
+        line["gpt_block"] = gpt_block_line(torch)
     print(json.dumps(line))
     return 0
 

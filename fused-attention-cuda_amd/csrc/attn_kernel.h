@@ -182,16 +182,16 @@ struct Attn {
   // skipped by the math -- so instead of zero-filling, the row index is clamped to N-1: every
   // address stays inside the tensor and the loads need no per-lane branch.
   __device__ static void load_tile(Staging& st, const Tio* kb, const Tio* vb, int k0, int N,
-                                   int tid) {
-    const Tio* kt = kb + static_cast<size_t>(k0) * D;
-    const Tio* vt = vb + static_cast<size_t>(k0) * D;
+                                   int ksn, int vsn, int tid) {
+    const Tio* kt = kb + static_cast<ptrdiff_t>(k0) * ksn;
+    const Tio* vt = vb + static_cast<ptrdiff_t>(k0) * vsn;
     const int last = N - 1 - k0;  // last valid tile-local key row (>= BC - 1 for a full tile)
 #pragma unroll
     for (int i = 0; i < kNK; ++i) {
       const int c = tid + i * kThreads;
       if ((kKChunks % kThreads == 0) || c < kKChunks) {
         const int row = min(c / kRowVecs, last);
-        st.kv[i] = *reinterpret_cast<const u32x4*>(kt + row * D + (c % kRowVecs) * kVec);
+        st.kv[i] = *reinterpret_cast<const u32x4*>(kt + row * ksn + (c % kRowVecs) * kVec);
       }
     }
 #pragma unroll
@@ -202,7 +202,7 @@ struct Attn {
         const Tio* src = vt + (c % kRowVecs) * kVec;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          st.vv[i][j] = *reinterpret_cast<const u32x4*>(src + min(row + j, last) * D);
+          st.vv[i][j] = *reinterpret_cast<const u32x4*>(src + min(row + j, last) * vsn);
         }
       }
     }
@@ -286,17 +286,17 @@ struct Attn {
     float l;   // this lane's partial row sum, relative to m
   };
 
-  __device__ static void load_q(WaveState& ws, const Tio* qb, int row, bool valid, int g) {
+  __device__ static void load_q(WaveState& ws, const Tio* qb, int row, int qsn, bool valid, int g) {
     if constexpr (kHalf) {
 #pragma unroll
       for (int s = 0; s < kQVecs; ++s) {
-        ws.qh[s] = valid ? *reinterpret_cast<const u32x4*>(qb + static_cast<size_t>(row) * D +
+        ws.qh[s] = valid ? *reinterpret_cast<const u32x4*>(qb + row * qsn +
                                                            16 * s + 8 * g)
                          : u32x4{0u, 0u, 0u, 0u};
       }
     } else {
       // fp32 MFMA k-slot mapping: lane half g covers head-dim [g*D/2, (g+1)*D/2).
-      const Tio* src = qb + static_cast<size_t>(row) * D + g * (D / 2);
+      const Tio* src = qb + row * qsn + g * (D / 2);
 #pragma unroll
       for (int j = 0; j < kQVecs; ++j) {
         if (!valid) {
@@ -481,11 +481,9 @@ struct Attn {
     const int hk = h / (a.H / a.Hkv);
     const int N = a.N;
 
-    const size_t q_off = (static_cast<size_t>(b) * a.H + h) * static_cast<size_t>(N) * D;
-    const size_t kv_off = (static_cast<size_t>(b) * a.Hkv + hk) * static_cast<size_t>(N) * D;
-    const Tio* qb = static_cast<const Tio*>(a.q) + q_off;
-    const Tio* kb = static_cast<const Tio*>(a.k) + kv_off;
-    const Tio* vb = static_cast<const Tio*>(a.v) + kv_off;
+    const Tio* qb = static_cast<const Tio*>(a.q) + b * a.qsb + h * a.qsh;
+    const Tio* kb = static_cast<const Tio*>(a.k) + b * a.ksb + hk * a.ksh;
+    const Tio* vb = static_cast<const Tio*>(a.v) + b * a.vsb + hk * a.vsh;
 
     const int i0 = qt * kBr;
     const int r0 = i0 + 32 * wave;  // this wave's first row
@@ -499,7 +497,7 @@ struct Attn {
     const int wave_end = wave_valid ? (a.causal ? min(N, r0 + 32) : N) : 0;
 
     WaveState ws;
-    load_q(ws, qb, row, wave_valid, g);
+    load_q(ws, qb, row, a.qsn, wave_valid, g);
 #pragma unroll
     for (int db = 0; db < kDB; ++db) ws.o[db] = f32x16{};
     ws.m = -__builtin_inff();
@@ -509,12 +507,12 @@ struct Attn {
     const float lazy_raw = lazy_log2<Tc>() / a.c;  // lazy-rescale threshold, raw score units
     Staging st;
     if constexpr (PREFETCH) {
-      load_tile(st, kb, vb, 0, N, tid);
+      load_tile(st, kb, vb, 0, N, a.ksn, a.vsn, tid);
       store_tile(st, lds, tid);
       __syncthreads();
       for (int t = 0; t < n_tiles; ++t) {
         const int k0 = t * BC;
-        if (t + 1 < n_tiles) load_tile(st, kb, vb, k0 + BC, N, tid);
+        if (t + 1 < n_tiles) load_tile(st, kb, vb, k0 + BC, N, a.ksn, a.vsn, tid);
         const int nvalid = max(0, min(kKB, (wave_end - k0 + 31) / 32));
         if (nvalid > 0) {
           const int diag = a.causal ? (r0 - k0) / 32 : -1;  // r0, k0 multiples of 32
@@ -527,7 +525,7 @@ struct Attn {
     } else {
       for (int t = 0; t < n_tiles; ++t) {
         const int k0 = t * BC;
-        load_tile(st, kb, vb, k0, N, tid);
+        load_tile(st, kb, vb, k0, N, a.ksn, a.vsn, tid);
         store_tile(st, lds, tid);
         __syncthreads();
         const int nvalid = max(0, min(kKB, (wave_end - k0 + 31) / 32));
@@ -544,7 +542,7 @@ struct Attn {
     const float lt = ws.l + __shfl_xor(ws.l, 32);
     if (!wave_valid) return;
     const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
-    Tio* orow = static_cast<Tio*>(a.o) + q_off + static_cast<size_t>(row) * D;
+    Tio* orow = static_cast<Tio*>(a.o) + b * a.osb + h * a.osh + row * a.osn;
 #pragma unroll
     for (int db = 0; db < kDB; ++db) {
 #pragma unroll

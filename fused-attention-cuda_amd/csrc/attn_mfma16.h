@@ -181,23 +181,25 @@ struct Fa16 {
     int off[kDmaPerWave];
   };
   template <bool IS_V>
-  __device__ static Dma dma_lane(int wave, int lane) {
+  __device__ static Dma dma_lane(int wave, int lane, int sn) {
     Dma d;
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
       const int pos = 64 * (wave + i * kWaves) + lane;  // chunk position in the tile
       d.row[i] = pos / kRowChunks;
-      d.off[i] = d.row[i] * D + 8 * ((pos % kRowChunks) ^ swz<IS_V>(d.row[i]));
+      d.off[i] = d.row[i] * sn + 8 * ((pos % kRowChunks) ^ swz<IS_V>(d.row[i]));
     }
     return d;
   }
 
-  // The tile of keys [k0, k0 + BC) of one tensor into `buf`. Rows past the last key (a partial
-  // last tile) read row N-1: every address stays in the tensor, and those rows sit in 32-key
-  // blocks that the math skips. The caller waits on vmcnt before the barrier that publishes it.
+  // The tile of keys [k0, k0 + BC) of one tensor (row stride sn) into `buf`. Rows past the last
+  // key (a partial last tile) read row N-1: every address stays in the tensor, and those rows
+  // sit in 32-key blocks that the math skips. The caller waits on vmcnt before the barrier that
+  // publishes it.
   template <bool IS_V>
-  __device__ static void dma_tile(T* buf, const T* gbase, const Dma& d, int k0, int N, int wave) {
-    const T* tile = gbase + static_cast<size_t>(k0) * D;
+  __device__ static void dma_tile(T* buf, const T* gbase, const Dma& d, int k0, int N, int sn,
+                                  int wave) {
+    const T* tile = gbase + static_cast<ptrdiff_t>(k0) * sn;
     if (k0 + BC <= N) {  // workgroup-uniform
 #pragma unroll
       for (int i = 0; i < kDmaPerWave; ++i) {
@@ -210,7 +212,7 @@ struct Fa16 {
       for (int i = 0; i < kDmaPerWave; ++i) {
         const int last = min(d.row[i], N - 1 - k0);
         __builtin_amdgcn_global_load_lds(
-            (const void __attribute__((address_space(1)))*)(tile + d.off[i] + (last - d.row[i]) * D),
+            (const void __attribute__((address_space(1)))*)(tile + d.off[i] + (last - d.row[i]) * sn),
             (void __attribute__((address_space(3)))*)(buf + 512 * (wave + i * kWaves)), 16, 0, 0);
       }
     }
@@ -495,11 +497,9 @@ struct Fa16 {
     const int hk = h / (a.H / a.Hkv);
     const int N = a.N;
 
-    const size_t q_off = (static_cast<size_t>(b) * a.H + h) * static_cast<size_t>(N) * D;
-    const size_t kv_off = (static_cast<size_t>(b) * a.Hkv + hk) * static_cast<size_t>(N) * D;
-    const T* qb = static_cast<const T*>(a.q) + q_off;
-    const T* kg = static_cast<const T*>(a.k) + kv_off;
-    const T* vg = static_cast<const T*>(a.v) + kv_off;
+    const T* qb = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
+    const T* kg = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
+    const T* vg = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
 
     const int i0 = qt * kBr;
     const int r0 = i0 + 32 * rg;  // this wave's first row
@@ -515,8 +515,7 @@ struct Fa16 {
     WaveState ws;
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
-      ws.q[st] = wave_valid ? *reinterpret_cast<const u32x4*>(qb + static_cast<size_t>(row) * D +
-                                                             16 * st + 8 * g)
+      ws.q[st] = wave_valid ? *reinterpret_cast<const u32x4*>(qb + row * a.qsn + 16 * st + 8 * g)
                             : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
@@ -530,8 +529,9 @@ struct Fa16 {
     T* const vbuf0 = lds + kBufs * kKElems;
     const KLane kl = k_lane(lane);
     const VLane vl = v_lane(lane);
-    const Dma dk = dma_lane<false>(wave, lane);
-    const Dma dv = dma_lane<true>(wave, lane);
+    const int ksn = a.ksn, vsn = a.vsn;
+    const Dma dk = dma_lane<false>(wave, lane, ksn);
+    const Dma dv = dma_lane<true>(wave, lane, vsn);
     auto kwave = [&](int buf) -> const T* { return kbuf0 + buf * kKElems + kbase * D; };
     auto vwave = [&](int buf) -> const T* { return vbuf0 + buf * kVElems + kbase * D; };
     // Valid 32-key blocks of tile t for this wave, and its causal diagonal block (-1 if none).
@@ -550,9 +550,9 @@ struct Fa16 {
       // reads K buffer (t+1)%2 and V buffer t%2 and refills K buffer t%2 with K(t+2) and V buffer
       // (t+1)%2 with V(t+1), each loaded into registers at the top of the iteration.
       // K(0), V(0) and K(1) in flight together (one memory round trip for the prologue).
-      dma_tile<false>(kbuf0, kg, dk, 0, N, wave);
-      dma_tile<true>(vbuf0, vg, dv, 0, N, wave);
-      if (n_tiles > 1) dma_tile<false>(kbuf0 + kKElems, kg, dk, BC, N, wave);
+      dma_tile<false>(kbuf0, kg, dk, 0, N, ksn, wave);
+      dma_tile<true>(vbuf0, vg, dv, 0, N, vsn, wave);
+      if (n_tiles > 1) dma_tile<false>(kbuf0 + kKElems, kg, dk, BC, N, ksn, wave);
       wait_dma();
       __syncthreads();
       f32x16 sa[kKB], sb[kKB];
@@ -572,8 +572,8 @@ struct Fa16 {
         (void)parity;
         constexpr bool kFull = decltype(full)::value;
         // K(t+2) and V(t+1) go straight into the buffers this iteration does not read.
-        if (t + 2 < n_tiles) dma_tile<false>(kbuf0 + (t & 1) * kKElems, kg, dk, (t + 2) * BC, N, wave);
-        if (t + 1 < n_tiles) dma_tile<true>(vbuf0 + ((t + 1) & 1) * kVElems, vg, dv, (t + 1) * BC, N, wave);
+        if (t + 2 < n_tiles) dma_tile<false>(kbuf0 + (t & 1) * kKElems, kg, dk, (t + 2) * BC, N, ksn, wave);
+        if (t + 1 < n_tiles) dma_tile<true>(vbuf0 + ((t + 1) & 1) * kVElems, vg, dv, (t + 1) * BC, N, vsn, wave);
         const T* kn = kwave((t + 1) & 1);
         const T* vc = vwave(t & 1);
         if constexpr (kFull) {
@@ -621,8 +621,8 @@ struct Fa16 {
     } else {
       f32x16 s[kKB];
       for (int t = 0; t < n_tiles; ++t) {
-        dma_tile<false>(kbuf0, kg, dk, t * BC, N, wave);
-        dma_tile<true>(vbuf0, vg, dv, t * BC, N, wave);
+        dma_tile<false>(kbuf0, kg, dk, t * BC, N, ksn, wave);
+        dma_tile<true>(vbuf0, vg, dv, t * BC, N, vsn, wave);
         wait_dma();
         __syncthreads();
         const int nv = nvalid_of(t);
@@ -678,7 +678,7 @@ struct Fa16 {
     const float lt = ws.l + __shfl_xor(ws.l, 32);
     if (!wave_valid) return;
     const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
-    T* orow = static_cast<T*>(a.o) + q_off + static_cast<size_t>(row) * D;
+    T* orow = static_cast<T*>(a.o) + b * a.osb + h * a.osh + row * a.osn;
 #pragma unroll
     for (int db = 0; db < kDB; ++db) {
 #pragma unroll

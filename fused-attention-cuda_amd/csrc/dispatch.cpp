@@ -152,7 +152,7 @@ int common_stage_checks(const char* tag, const void* q, const void* k, const voi
 }
 
 KArgs make_args(const void* q, const void* k, const void* v, void* o, float* lse,
-                const fa_params& p) {
+                const fa_params& p, const Strides& st) {
   KArgs a{};
   a.q = q;
   a.k = k;
@@ -167,7 +167,40 @@ KArgs make_args(const void* q, const void* k, const void* v, void* o, float* lse
   a.scale = p.scale;
   a.c = p.scale * kLog2e;  // folded once per launch (ref:include/fa/softmax_math.cuh:29-32)
   a.causal = p.causal ? 1 : 0;
+  a.qsb = st.q.b;
+  a.qsh = st.q.h;
+  a.qsn = static_cast<int>(st.q.n);
+  a.ksb = st.k.b;
+  a.ksh = st.k.h;
+  a.ksn = static_cast<int>(st.k.n);
+  a.vsb = st.v.b;
+  a.vsh = st.v.h;
+  a.vsn = static_cast<int>(st.v.n);
+  a.osb = st.o.b;
+  a.osh = st.o.h;
+  a.osn = static_cast<int>(st.o.n);
   return a;
+}
+
+// Dense [B, heads, N, D] strides.
+fa_strides dense_strides(const fa_params& p, int heads) {
+  fa_strides s;
+  s.n = p.D;
+  s.h = static_cast<long long>(p.N) * p.D;
+  s.b = static_cast<long long>(heads) * s.h;
+  return s;
+}
+
+// Returns nullptr when the strides are usable (see fa_forward_strided in the header).
+const char* check_strides(const fa_strides* s, int dtype, const fa_params& p) {
+  if (s == nullptr) return "strides must be non-null";
+  if (s->b < 0 || s->h < 0 || s->n < 0) return "strides must be >= 0";
+  const long long per16 = 16 / static_cast<long long>(fa_dtype_size(dtype));
+  if (s->b % per16 != 0 || s->h % per16 != 0 || s->n % per16 != 0)
+    return "strides must be multiples of 16 bytes";
+  if (static_cast<long long>(p.N - 1) * s->n + p.D > 0x7fffffffLL)
+    return "row offsets within a head must fit 32 bits";
+  return nullptr;
 }
 
 const Variant* find_variant(VariantList list, int D, int br, int bc) {
@@ -219,13 +252,14 @@ bool supports(int dtype, int D, int arch) {
 }
 
 int forward(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
-            const fa_params& p, const Overrides& dbg, int arch, hipStream_t stream) {
+            const fa_params& p, const Strides& st, const Overrides& dbg, int arch,
+            hipStream_t stream) {
   if (!supports(dtype, p.D, arch)) return static_cast<int>(hipErrorNotSupported);
   const int rc = common_stage_checks("stage5", q, k, v, o, lse, p);
   if (rc != 0) return rc;
   const int br = dbg.block_m != 0 ? dbg.block_m : kDefaultBr;
   const int bc = dbg.block_n != 0 ? dbg.block_n : default_bc_mfma(p.D);
-  const KArgs a = make_args(q, k, v, o, lse, p);
+  const KArgs a = make_args(q, k, v, o, lse, p, st);
   const VariantList list = dtype == FA_DTYPE_F16 ? variants_s5_f16() : variants_s5_bf16();
   return launch_selected("stage5", list, br, bc, a, p.D, stream);
 }
@@ -238,7 +272,8 @@ namespace stage4 {
 bool supports(int dtype, int D, int arch) { return stage5::supports(dtype, D, arch); }
 
 int forward(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
-            const fa_params& p, const Overrides& dbg, int arch, hipStream_t stream) {
+            const fa_params& p, const Strides& st, const Overrides& dbg, int arch,
+            hipStream_t stream) {
   if (!supports(dtype, p.D, arch)) return static_cast<int>(hipErrorNotSupported);
   const int rc = common_stage_checks("stage4", q, k, v, o, lse, p);
   if (rc != 0) return rc;
@@ -247,7 +282,7 @@ int forward(int dtype, const void* q, const void* k, const void* v, void* o, flo
                  kDefaultBr);
   }
   const int bc = dbg.block_n != 0 ? dbg.block_n : default_bc_mfma(p.D);
-  const KArgs a = make_args(q, k, v, o, lse, p);
+  const KArgs a = make_args(q, k, v, o, lse, p, st);
   const VariantList list = dtype == FA_DTYPE_F16 ? variants_s4_f16() : variants_s4_bf16();
   return launch_selected("stage4", list, kDefaultBr, bc, a, p.D, stream);
 }
@@ -263,7 +298,8 @@ bool supports(int dtype, int D, int arch) {
 }
 
 int forward(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
-            const fa_params& p, const Overrides& dbg, int arch, hipStream_t stream) {
+            const fa_params& p, const Strides& st, const Overrides& dbg, int arch,
+            hipStream_t stream) {
   if (!supports(dtype, p.D, arch)) return static_cast<int>(hipErrorNotSupported);
   const int rc = common_stage_checks("stage3", q, k, v, o, lse, p);
   if (rc != 0) return rc;
@@ -272,12 +308,38 @@ int forward(int dtype, const void* q, const void* k, const void* v, void* o, flo
                  kDefaultBr);
   }
   const int bc = dbg.block_n != 0 ? dbg.block_n : kDefaultBcF32;
-  const KArgs a = make_args(q, k, v, o, lse, p);
+  const KArgs a = make_args(q, k, v, o, lse, p, st);
   const VariantList list = dtype == FA_DTYPE_F32 ? variants_s3_f32() : variants_s3_f16();
   return launch_selected("stage3", list, kDefaultBr, bc, a, p.D, stream);
 }
 }  // namespace stage3
 
+}  // namespace fa
+
+namespace fa {
+namespace {
+// The body of fa_forward / fa_forward_strided once the arguments are validated.
+int forward_impl(int impl, int dtype, const void* q, const void* k, const void* v, void* o,
+                 float* lse, void* workspace, const fa_params* p, const Strides& st,
+                 hipStream_t stream) {
+  int arch = 0;
+  const int rc = fa_current_arch(&arch);
+  if (rc != 0) return rc;
+  const fa::StageEntry* e = fa::find_stage(impl);
+  if (e == nullptr || e->forward == nullptr || !fa_impl_supports(impl, dtype, p->D, arch)) {
+    if (fa::verbose()) {
+      std::fprintf(stderr, "fa_forward: %s/%s/D=%d not supported on gfx%d in this build\n",
+                   fa_impl_name(impl), fa_dtype_name(dtype), p->D, arch);
+    }
+    return static_cast<int>(hipErrorNotSupported);
+  }
+  if (fa_workspace_bytes(impl, dtype, p) > 0 && workspace == nullptr) {
+    if (fa::verbose()) std::fprintf(stderr, "fa_forward: workspace required but NULL\n");
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  return e->forward(dtype, q, k, v, o, lse, *p, st, fa::overrides_now(), arch, stream);
+}
+}  // namespace
 }  // namespace fa
 
 // =============================================================================================
@@ -306,28 +368,36 @@ int fa_current_arch(int* arch) {
   return static_cast<int>(hipSuccess);
 }
 
+
 int fa_forward(int impl, int dtype, const void* q, const void* k, const void* v, void* o,
                float* lse, void* workspace, const fa_params* p, hipStream_t stream) {
   if (const char* why = fa::validate(dtype, q, k, v, o, lse, p, impl)) {
     if (fa::verbose()) std::fprintf(stderr, "fa_forward: invalid params: %s\n", why);
     return static_cast<int>(hipErrorInvalidValue);
   }
-  int arch = 0;
-  const int rc = fa_current_arch(&arch);
-  if (rc != 0) return rc;
-  const fa::StageEntry* e = fa::find_stage(impl);
-  if (e == nullptr || e->forward == nullptr || !fa_impl_supports(impl, dtype, p->D, arch)) {
-    if (fa::verbose()) {
-      std::fprintf(stderr, "fa_forward: %s/%s/D=%d not supported on gfx%d in this build\n",
-                   fa_impl_name(impl), fa_dtype_name(dtype), p->D, arch);
-    }
-    return static_cast<int>(hipErrorNotSupported);
-  }
-  if (fa_workspace_bytes(impl, dtype, p) > 0 && workspace == nullptr) {
-    if (fa::verbose()) std::fprintf(stderr, "fa_forward: workspace required but NULL\n");
+  fa::Strides st;
+  st.q = st.o = fa::dense_strides(*p, p->H);
+  st.k = st.v = fa::dense_strides(*p, p->Hkv);
+  return fa::forward_impl(impl, dtype, q, k, v, o, lse, workspace, p, st, stream);
+}
+
+int fa_forward_strided(int impl, int dtype, const void* q, const fa_strides* q_strides,
+                       const void* k, const fa_strides* k_strides, const void* v,
+                       const fa_strides* v_strides, void* o, const fa_strides* o_strides,
+                       float* lse, void* workspace, const fa_params* p, hipStream_t stream) {
+  const char* why = fa::validate(dtype, q, k, v, o, lse, p, impl);
+  const fa_strides* all[4] = {q_strides, k_strides, v_strides, o_strides};
+  for (int i = 0; why == nullptr && i < 4; ++i) why = fa::check_strides(all[i], dtype, *p);
+  if (why != nullptr) {
+    if (fa::verbose()) std::fprintf(stderr, "fa_forward_strided: invalid params: %s\n", why);
     return static_cast<int>(hipErrorInvalidValue);
   }
-  return e->forward(dtype, q, k, v, o, lse, *p, fa::overrides_now(), arch, stream);
+  fa::Strides st;
+  st.q = *q_strides;
+  st.k = *k_strides;
+  st.v = *v_strides;
+  st.o = *o_strides;
+  return fa::forward_impl(impl, dtype, q, k, v, o, lse, workspace, p, st, stream);
 }
 
 size_t fa_workspace_bytes(int impl, int /*dtype*/, const fa_params* p) {

@@ -18,10 +18,13 @@
 #include <c10/hip/HIPFunctions.h>
 #include <torch/library.h>
 
+#include <algorithm>
+#include <array>
 #include <cstdint>
 #include <limits>
 #include <string>
 #include <tuple>
+#include <vector>
 
 #include "fa/attention.h"
 
@@ -70,9 +73,10 @@ int checked_int(int64_t v, const char* what) {
 }
 
 // The frozen input contract; every violation is a RuntimeError with a message, never a device
-// fault (ref:python/fused_attn/ext.cpp:82-126).
+// fault (ref:python/fused_attn/ext.cpp:82-126). `dense` is the reference's contiguity rule;
+// forward_strided relaxes it to a contiguous head dim with 16-byte-aligned strides.
 fa_params make_params(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
-                      bool is_causal, double scale) {
+                      bool is_causal, double scale, bool dense = true) {
   TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(),
               "fused_attn: q, k, v must be CUDA (ROCm/HIP device) tensors");
   TORCH_CHECK(q.device() == k.device() && q.device() == v.device(),
@@ -80,8 +84,21 @@ fa_params make_params(const at::Tensor& q, const at::Tensor& k, const at::Tensor
   TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4,
               "fused_attn: q, k, v must be [B, H, N, D]; got ", q.dim(), "-D, ", k.dim(), "-D, ",
               v.dim(), "-D");
-  TORCH_CHECK(q.is_contiguous() && k.is_contiguous() && v.is_contiguous(),
-              "fused_attn: q, k, v must be contiguous [B, H, N, D] (call .contiguous())");
+  if (dense) {
+    TORCH_CHECK(q.is_contiguous() && k.is_contiguous() && v.is_contiguous(),
+                "fused_attn: q, k, v must be contiguous [B, H, N, D] (call .contiguous())");
+  } else {
+    for (const at::Tensor* t : {&q, &k, &v}) {
+      TORCH_CHECK(t->stride(3) == 1 || t->size(3) == 1,
+                  "fused_attn: forward_strided needs a contiguous head dim (stride(-1) == 1)");
+      const int64_t per16 = 16 / static_cast<int64_t>(t->element_size());
+      for (int d = 0; d < 3; ++d) {
+        TORCH_CHECK(t->stride(d) >= 0 && t->stride(d) % per16 == 0,
+                    "fused_attn: forward_strided needs batch/head/row strides that are multiples "
+                    "of 16 bytes, got stride(", d, ")=", t->stride(d));
+      }
+    }
+  }
   // The kernels use 16-byte vector loads; a contiguous offset view such as t[2:] is not 16-byte
   // aligned and is refused here rather than faulting inside the kernel.
   for (const at::Tensor* t : {&q, &k, &v}) {
@@ -153,6 +170,58 @@ std::tuple<at::Tensor, at::Tensor> run_stage(const at::Tensor& q, const at::Tens
   return std::make_tuple(std::move(o), std::move(lse));
 }
 
+fa_strides strides_of(const at::Tensor& t) {
+  fa_strides s;
+  s.b = t.stride(0);
+  s.h = t.stride(1);
+  s.n = t.stride(2);
+  return s;
+}
+
+// A dense tensor with q's shape whose memory order follows q's strides (outermost first): for
+// the [B, H, N, D] view of a [B, N, H, D] buffer the result is a [B, N, H, D] buffer seen as
+// [B, H, N, D], so the caller's transpose back to [B, N, H*D] is free. Contiguous q gives a
+// contiguous result. ops.py's fake kernel applies the same rule.
+at::Tensor empty_in_layout_of(const at::Tensor& q) {
+  std::array<int64_t, 4> order = {0, 1, 2, 3};
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int64_t a, int64_t b) { return q.stride(a) > q.stride(b); });
+  std::vector<int64_t> sizes, inverse(4);
+  for (int i = 0; i < 4; ++i) {
+    sizes.push_back(q.size(order[i]));
+    inverse[order[i]] = i;
+  }
+  return at::empty(sizes, q.options()).permute(inverse);
+}
+
+// forward_strided: as forward (best stage, O only) over strided views (fa_forward_strided). No
+// counterpart in the reference (its op requires dense tensors); it removes the layout copies
+// around the op in a transformer block.
+at::Tensor forward_strided_cuda(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                bool is_causal, double scale) {
+  const fa_params p = make_params(q, k, v, is_causal, scale, /*dense=*/false);
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  const int dtype = to_fa_dtype(q.scalar_type());
+  const int arch = current_arch();
+  int stage = 0;
+  for (int s = static_cast<int>(kMaxStage); s >= static_cast<int>(kMinStage) && stage == 0; --s) {
+    if (fa_impl_supports(s, dtype, p.D, arch)) stage = s;
+  }
+  TORCH_CHECK(stage >= kFirstLseStage, "fused_attn: no stage is implemented for ",
+              fa_dtype_name(dtype), " D=", p.D, " on gfx", arch);
+  at::Tensor o = empty_in_layout_of(q);
+  at::Tensor lse = at::empty({p.B, p.H, p.N}, q.options().dtype(at::kFloat));
+  const fa_strides qs = strides_of(q), ks = strides_of(k), vs = strides_of(v), os = strides_of(o);
+  const hipStream_t stream =
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.device().index()).stream();
+  const int err = fa_forward_strided(stage, dtype, q.data_ptr(), &qs, k.data_ptr(), &ks,
+                                     v.data_ptr(), &vs, o.data_ptr(), &os, lse.data_ptr<float>(),
+                                     nullptr, &p, stream);
+  TORCH_CHECK(err == 0, "fused_attn: stage ", stage, " (", fa_impl_name(stage),
+              ") failed: ", fa_error_string(err));
+  return o;
+}
+
 // forward: the highest implemented stage for (dtype, D, arch) (ref:python/fused_attn/ext.cpp:171-188).
 at::Tensor forward_cuda(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                         bool is_causal, double scale) {
@@ -200,6 +269,8 @@ TORCH_LIBRARY(fused_attn, m) {
   m.def(
       "forward_stage(Tensor q, Tensor k, Tensor v, bool is_causal, float scale, int stage)"
       " -> (Tensor, Tensor)");
+  // Extension beyond the reference's frozen schemas: strided q/k/v views.
+  m.def("forward_strided(Tensor q, Tensor k, Tensor v, bool is_causal, float scale) -> Tensor");
   // Scalar-only ops have no dispatch key: their kernels are catch-alls.
   m.def("set_debug_overrides(int block_m, int block_n) -> ()", &set_debug_overrides_op);
   m.def("impl_supports(int stage, str dtype, int D) -> bool", &impl_supports_op);
@@ -209,6 +280,7 @@ TORCH_LIBRARY(fused_attn, m) {
 TORCH_LIBRARY_IMPL(fused_attn, CUDA, m) {
   m.impl("forward", &forward_cuda);
   m.impl("forward_stage", &forward_stage_cuda);
+  m.impl("forward_strided", &forward_strided_cuda);
 }
 
 // Importing the .so runs the TORCH_LIBRARY static initialisers; the module exports nothing.

@@ -37,6 +37,11 @@ struct KArgs {
   float scale;   // softmax scale (for lse = m*scale + ln l)
   float c;       // scale * log2(e), folded into every exp2
   int causal;
+  // Element strides of q, k, v, o: per batch and per head (64-bit) and per row (a row offset
+  // within one head fits 32 bits; the launcher checks). The head dim is contiguous. lse is
+  // always dense [B, H, N].
+  long long qsb, qsh, ksb, ksh, vsb, vsh, osb, osh;
+  int qsn, ksn, vsn, osn;
 };
 
 // One instantiated (D, BR, BC) kernel of a stage, and the table of them per (stage, dtype).
@@ -58,15 +63,21 @@ VariantList variants_s4_bf16();  // attn_bf16.hip
 VariantList variants_s3_f32();   // attn_f32.hip (fp32 I/O)
 VariantList variants_s3_f16();   // attn_f32.hip (fp16 I/O, fp32 compute)
 
+// Strides of the four [B, H, N, D] operands (fa_strides of include/fa/attention.h).
+struct Strides {
+  fa_strides q, k, v, o;
+};
+
 using StageForwardFn = int (*)(int dtype, const void* q, const void* k, const void* v, void* o,
-                               float* lse, const fa_params& p, const Overrides& dbg, int arch,
-                               hipStream_t stream);
+                               float* lse, const fa_params& p, const Strides& st,
+                               const Overrides& dbg, int arch, hipStream_t stream);
 using StageSupportsFn = bool (*)(int dtype, int D, int arch);
 
 #define FA_DECLARE_STAGE(ns)                                                                   \
   namespace ns {                                                                               \
   int forward(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,     \
-              const fa_params& p, const Overrides& dbg, int arch, hipStream_t stream);         \
+              const fa_params& p, const Strides& st, const Overrides& dbg, int arch,           \
+              hipStream_t stream);                                                             \
   bool supports(int dtype, int D, int arch);                                                   \
   }
 FA_DECLARE_STAGE(stage3)  // attn_f32.hip   fa_s3_fused  : fp32 MFMA compute, fp32/fp16 I/O

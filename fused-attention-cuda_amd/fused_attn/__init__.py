@@ -17,6 +17,9 @@ Ops (schemas as in the reference, ref:python/fused_attn/ext.cpp:220-230)::
 
     torch.ops.fused_attn.forward(q, k, v, is_causal, scale) -> Tensor
     torch.ops.fused_attn.forward_stage(q, k, v, is_causal, scale, stage) -> (Tensor, Tensor)
+
+plus one extension: ``torch.ops.fused_attn.forward_strided(q, k, v, is_causal, scale) -> Tensor``
+over strided views (no counterpart in the reference).
 """
 
 from __future__ import annotations
@@ -32,6 +35,7 @@ __all__ = [
     "__version__",
     "forward",
     "forward_stage",
+    "forward_strided",
     "impl_name",
     "impl_supports",
     "is_available",
@@ -86,6 +90,16 @@ def forward_stage(q: Tensor, k: Tensor, v: Tensor, stage: int, is_causal: bool =
     _require_ext()
     return torch.ops.fused_attn.forward_stage(q, k, v, bool(is_causal),
                                               _resolve_scale(q, scale), int(stage))
+
+
+def forward_strided(q: Tensor, k: Tensor, v: Tensor, is_causal: bool = False,
+                    scale: float | None = None) -> Tensor:
+    """``forward`` over strided [B, H, N, D] views (head dim contiguous, batch/head/row strides
+    multiples of 16 bytes), e.g. ``qkv.view(B, N, 3, H, D)[:, :, 0].transpose(1, 2)`` with no copy.
+    The output is dense in q's memory order (see ``ops.empty_in_layout_of``). An extension of the
+    reference op surface, which only takes contiguous tensors."""
+    _require_ext()
+    return torch.ops.fused_attn.forward_strided(q, k, v, bool(is_causal), _resolve_scale(q, scale))
 
 
 def impl_supports(stage: int, dtype: torch.dtype, head_dim: int) -> bool:

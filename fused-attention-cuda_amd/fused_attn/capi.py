@@ -28,7 +28,7 @@ DTYPE_CODES = {torch.float32: FA_DTYPE_F32, torch.float16: FA_DTYPE_F16,
                torch.bfloat16: FA_DTYPE_BF16}
 
 # Every function include/fa/attention.h declares, in declaration order.
-EXPORTS = ("fa_forward", "fa_workspace_bytes", "fa_impl_supports", "fa_set_debug_overrides",
+EXPORTS = ("fa_forward", "fa_forward_strided", "fa_workspace_bytes", "fa_impl_supports", "fa_set_debug_overrides",
            "fa_get_debug_overrides", "fa_impl_name", "fa_dtype_name", "fa_dtype_size",
            "fa_current_arch", "fa_error_string")
 
@@ -39,6 +39,12 @@ class FaParams(ctypes.Structure):
     _fields_ = [("B", ctypes.c_int), ("H", ctypes.c_int), ("Hkv", ctypes.c_int),
                 ("N", ctypes.c_int), ("D", ctypes.c_int), ("scale", ctypes.c_float),
                 ("causal", ctypes.c_bool)]
+
+
+class FaStrides(ctypes.Structure):
+    """``fa_strides`` (include/fa/attention.h): per batch, per head, per row, in elements."""
+
+    _fields_ = [("b", ctypes.c_longlong), ("h", ctypes.c_longlong), ("n", ctypes.c_longlong)]
 
 
 _lib: ctypes.CDLL | None = None
@@ -56,6 +62,10 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     vp, ci = ctypes.c_void_p, ctypes.c_int
     lib.fa_forward.argtypes = [ci, ci, vp, vp, vp, vp, vp, vp, ctypes.POINTER(FaParams), vp]
     lib.fa_forward.restype = ci
+    sp = ctypes.POINTER(FaStrides)
+    lib.fa_forward_strided.argtypes = [ci, ci, vp, sp, vp, sp, vp, sp, vp, sp, vp, vp,
+                                       ctypes.POINTER(FaParams), vp]
+    lib.fa_forward_strided.restype = ci
     lib.fa_workspace_bytes.argtypes = [ci, ci, ctypes.POINTER(FaParams)]
     lib.fa_workspace_bytes.restype = ctypes.c_size_t
     lib.fa_impl_supports.argtypes = [ci, ci, ci, ci]
@@ -111,3 +121,21 @@ def forward(impl: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: tor
     s = stream if stream is not None else torch.cuda.current_stream(q.device)
     return forward_raw(impl, DTYPE_CODES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
                        o.data_ptr(), 0 if lse is None else lse.data_ptr(), 0, p, s.cuda_stream)
+
+
+def strides_of(t: torch.Tensor) -> FaStrides:
+    return FaStrides(t.stride(0), t.stride(1), t.stride(2))
+
+
+def forward_strided(impl: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+                    lse: torch.Tensor, is_causal: bool, scale: float,
+                    stream: torch.cuda.Stream | None = None) -> int:
+    """``fa_forward_strided`` on torch views (their own strides); returns the hipError_t value."""
+    b, h, n, d = q.shape
+    p = params(b, h, k.shape[1], n, d, scale, is_causal)
+    s = stream if stream is not None else torch.cuda.current_stream(q.device)
+    qs, ks, vs, os_ = strides_of(q), strides_of(k), strides_of(v), strides_of(o)
+    return load().fa_forward_strided(impl, DTYPE_CODES[q.dtype], q.data_ptr(), ctypes.byref(qs),
+                                     k.data_ptr(), ctypes.byref(ks), v.data_ptr(),
+                                     ctypes.byref(vs), o.data_ptr(), ctypes.byref(os_),
+                                     lse.data_ptr(), None, ctypes.byref(p), s.cuda_stream)

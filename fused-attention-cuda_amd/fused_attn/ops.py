@@ -57,6 +57,25 @@ def _fake_forward_stage(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, scale:
     return o, lse
 
 
+def empty_in_layout_of(q: Tensor) -> Tensor:
+    """A dense tensor of q's shape whose memory order follows q's strides (outermost first) --
+    the output layout of ``forward_strided`` (csrc/ext.cpp ``empty_in_layout_of``): for the
+    [B, H, N, D] view of a [B, N, H, D] buffer it is a [B, N, H, D] buffer seen as [B, H, N, D]."""
+    order = sorted(range(4), key=lambda d: -q.stride(d))  # stable: ties keep dimension order
+    out = q.new_empty([q.shape[d] for d in order])
+    inverse = [order.index(d) for d in range(4)]
+    return out.permute(inverse)
+
+
+def _fake_forward_strided(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, scale: float) -> Tensor:
+    torch._check(q.dim() == 4 and k.dim() == 4 and v.dim() == 4, lambda: "q/k/v must be [B,H,N,D]")
+    b, h, n, d = q.shape
+    torch._check(d == 64 or d == 128, lambda: f"D must be 64 or 128, got {d}")
+    torch._check(n % 32 == 0, lambda: f"N must be a multiple of 32, got {n}")
+    torch._check(q.dtype == k.dtype and q.dtype == v.dtype, lambda: "q/k/v must share one dtype")
+    return empty_in_layout_of(q)
+
+
 def register_fakes() -> None:
     """Register the fake kernels (idempotent; requires ``fused_attn._C`` to be loaded)."""
     global _registered
@@ -64,6 +83,7 @@ def register_fakes() -> None:
         return
     torch.library.register_fake("fused_attn::forward", _fake_forward)
     torch.library.register_fake("fused_attn::forward_stage", _fake_forward_stage)
+    torch.library.register_fake("fused_attn::forward_strided", _fake_forward_strided)
     _registered = True
 
 

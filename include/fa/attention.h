@@ -68,6 +68,28 @@ typedef struct fa_params {
 FA_API int fa_forward(int impl, int dtype, const void* q, const void* k, const void* v, void* o,
                float* lse, void* workspace, const fa_params* p, hipStream_t stream);
 
+/* Element strides of one [B, H, N, D] operand: per batch (b), per head (h) and per row (n).
+ * The head dimension D is always contiguous (stride 1). A dense tensor has n = D, h = N*D,
+ * b = H*N*D (Hkv in place of H for k and v). */
+typedef struct fa_strides {
+  long long b;
+  long long h;
+  long long n;
+} fa_strides;
+
+/* fa_forward over strided q/k/v/o views, e.g. the [B, H, N, D] view of a [B, N, H, D] buffer
+ * (the head split of a fused QKV projection, transposed without a copy). No counterpart in the
+ * reference, whose API takes dense tensors only (ref:include/fa/attention.cuh:38-45); it is the
+ * "strided inputs" extension of its op. Same contract as fa_forward otherwise, plus: every stride
+ * is >= 0 and a multiple of 16 bytes, so every row start is 16-byte aligned; (N-1)*n + D fits a
+ * 32-bit int for every operand; o must not overlap q, k or v; lse stays dense [B, H, N].
+ * Returns hipErrorInvalidValue for strides that break these rules. */
+FA_API int fa_forward_strided(int impl, int dtype, const void* q, const fa_strides* q_strides,
+                              const void* k, const fa_strides* k_strides, const void* v,
+                              const fa_strides* v_strides, void* o, const fa_strides* o_strides,
+                              float* lse, void* workspace, const fa_params* p,
+                              hipStream_t stream);
+
 /* Replaces fa::workspace_bytes (ref:include/fa/attention.cuh:51, ref:src/dispatch.cu:163-168):
  * 2*B*H*N*N*4 for the materialising stages 1-2, 0 for the fused stages. */
 FA_API size_t fa_workspace_bytes(int impl, int dtype, const fa_params* p);
