@@ -218,6 +218,19 @@ struct Fa16 {
     }
   }
 
+  // dma_tile for a tile known to lie inside the tensor (k0 + BC <= N): no clamp, no branch.
+  template <bool IS_V>
+  __device__ static void dma_tile_full(T* buf, const T* gbase, const Dma& d, int k0, int sn,
+                                       int wave) {
+    const T* tile = gbase + static_cast<ptrdiff_t>(k0) * sn;
+#pragma unroll
+    for (int i = 0; i < kDmaPerWave; ++i) {
+      __builtin_amdgcn_global_load_lds(
+          (const void __attribute__((address_space(1)))*)(tile + d.off[i]),
+          (void __attribute__((address_space(3)))*)(buf + 512 * (wave + i * kWaves)), 16, 0, 0);
+    }
+  }
+
   // Waits until this wave's LDS-DMA loads have landed (vmcnt(0); expcnt and lgkmcnt untouched).
   __device__ static void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -429,10 +442,14 @@ struct Fa16 {
 
   // The steady-state step on full tiles: S(t+1) = K(t+1) Q^T on MFMA, interleaved with the
   // exponentials of S(t); every LDS read of the step (K rows of t+1 and the V^T operands of t) is
-  // issued up front so that no MFMA waits on LDS latency; then the P(t) V(t) MFMAs.
+  // issued up front so that no MFMA waits on LDS latency; then the P(t) V(t) MFMAs. `prefetch`
+  // issues the LDS-DMA of later tiles after those reads: the compiler cannot tell a DMA's LDS
+  // target from the buffers read here and makes any LDS read that follows a DMA wait for it
+  // (vmcnt(0)), which would expose the whole memory latency in every step.
+  template <typename Prefetch>
   __device__ static void step_full(WaveState& ws, f32x16 (&s_cur)[kKB], f32x16 (&s_nxt)[kKB],
                                    Probs& P, const T* Kn, const T* Vc, const KLane& kl,
-                                   const VLane& vl, float c, int lane) {
+                                   const VLane& vl, float c, int lane, Prefetch&& prefetch) {
     VOps va;
     qk<true>(s_nxt, ws, Kn, kKB, kl);
 #pragma unroll
@@ -443,17 +460,19 @@ struct Fa16 {
         for (int db = 0; db < kDB; ++db) va[kb][h][db] = v_operand(Vc, vl, kb, h, db);
       }
     }
+    prefetch();
     float mx = 0.f;
     const float rs = softmax_exp<true>(ws, s_cur, P, mx, kKB, -1, c, lane);
-    // Issue order for the region: the K reads, then the V^T reads, then one MFMA of S(t+1) per
-    // group of VALU ops. While an MFMA runs in the matrix core the wave keeps issuing independent
-    // VALU work (issue is in order, so a cluster of MFMAs would stall it).
+    // Issue order for the region: the K reads, then the V^T reads, then the DMA, then one MFMA of
+    // S(t+1) per group of VALU ops. While an MFMA runs in the matrix core the wave keeps issuing
+    // independent VALU work (issue is in order, so a cluster of MFMAs would stall it).
     constexpr int kMfma = kKB * (D / 16);
     constexpr int kVReads = kKB * 2 * kDB * 2;
     constexpr int kValu = (kF16 ? 48 : 66) * kKB;
     constexpr int kPer = (kValu + kMfma - 1) / kMfma;
     __builtin_amdgcn_sched_group_barrier(0x100, kMfma, 0);    // DS reads: K rows
     __builtin_amdgcn_sched_group_barrier(0x100, kVReads, 0);  // DS reads: V^T operands
+    __builtin_amdgcn_sched_group_barrier(0x020, 2 * kDmaPerWave, 0);  // VMEM: the DMA
 #pragma unroll
     for (int i = 0; i < kMfma; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x002, kPer, 0);  // VALU
@@ -572,13 +591,17 @@ struct Fa16 {
         (void)parity;
         constexpr bool kFull = decltype(full)::value;
         // K(t+2) and V(t+1) go straight into the buffers this iteration does not read.
-        if (t + 2 < n_tiles) dma_tile<false>(kbuf0 + (t & 1) * kKElems, kg, dk, (t + 2) * BC, N, ksn, wave);
-        if (t + 1 < n_tiles) dma_tile<true>(vbuf0 + ((t + 1) & 1) * kVElems, vg, dv, (t + 1) * BC, N, vsn, wave);
         const T* kn = kwave((t + 1) & 1);
         const T* vc = vwave(t & 1);
         if constexpr (kFull) {
-          step_full(ws, s_cur, s_nxt, P, kn, vc, kl, vl, c, lane);
+          // Steady steps have K(t+2) and V(t+1) inside the tensor (see n_steady).
+          step_full(ws, s_cur, s_nxt, P, kn, vc, kl, vl, c, lane, [&] {
+            dma_tile_full<false>(kbuf0 + (t & 1) * kKElems, kg, dk, (t + 2) * BC, ksn, wave);
+            dma_tile_full<true>(vbuf0 + ((t + 1) & 1) * kVElems, vg, dv, (t + 1) * BC, vsn, wave);
+          });
         } else {
+          if (t + 2 < n_tiles) dma_tile<false>(kbuf0 + (t & 1) * kKElems, kg, dk, (t + 2) * BC, N, ksn, wave);
+          if (t + 1 < n_tiles) dma_tile<true>(vbuf0 + ((t + 1) & 1) * kVElems, vg, dv, (t + 1) * BC, N, vsn, wave);
           const int nv = nvalid_of(t);
           const int dg = diag_of(t, nv);
           const int nv_nxt = (t + 1 < n_tiles) ? nvalid_of(t + 1) : 0;
@@ -600,7 +623,8 @@ struct Fa16 {
       // Tiles [0, n_full) are full for every wave and carry no diagonal (workgroup-uniform): key
       // tile t is complete below the workgroup's first row (causal) or below N.
       const int n_full = (a.causal ? i0 : N) / BC;
-      const int n_steady = max(0, min(n_tiles, n_full) - 1);
+      // Steady step t also needs K(t+2) to be a whole tile inside the tensor: t + 3 <= N / BC.
+      const int n_steady = max(0, min(min(n_tiles, n_full) - 1, N / BC - 2));
       // Unrolled by two so the S(t) / S(t+1) register sets swap roles without copies; the steady
       // loop and the tail loop get independent register assignments.
       int t = 0;
