@@ -161,13 +161,23 @@ struct Fa16 {
   static_assert(kDmaInsts % kWaves == 0, "every wave issues the same number of DMA instructions");
 
   // LDS layout of a K/V tile: BC rows of D elements, unpadded; the 16-byte chunk c of row r
-  // lives at chunk position c ^ swz(r). K uses swz(r) = r & 7: the 8 rows that 8 consecutive
-  // lanes read for one MFMA operand land on 8 distinct 16-byte bank groups. V uses
-  // swz(r) = 2 (r & 3): the 4 rows of one 16-lane transpose read land their 32-byte segments on
-  // 4 distinct bank ranges.
+  // lives at chunk position c ^ swz(r). The swizzles were chosen by measuring the read rate of
+  // each operand pattern on gfx950 (8 waves per CU, LDS bytes per clock):
+  //   K, 16 consecutive lanes read 16 consecutive rows (ds_read_b128): D = 64 rows are 128 bytes,
+  //     so a row pair spans the banks once and swz(r) = (r >> 1) & 7 gives the 16 lanes 16
+  //     distinct 16-byte bank groups (234 B/clk; r & 7 leaves a 2-way conflict, 147 B/clk);
+  //     D = 128 rows are 256 bytes and swz(r) = r & 15 does the same (242 against 146 B/clk).
+  //   V, one 16-lane transpose read covers 4 consecutive rows: swz(r) = 2 (r & 3) at D = 64
+  //     (129 B/clk, the best measured) and 4 (r & 3) at D = 128 (178 against 149 B/clk).
+  // Every swizzle depends on r % 32 only, so a lane's offsets inside a 32-key block are
+  // loop-invariant (blocks start at multiples of 32).
   template <bool IS_V>
   __device__ static int swz(int row) {
-    return IS_V ? 2 * (row & 3) : (row & 7);
+    if constexpr (IS_V) {
+      return (D == 64 ? 2 : 4) * (row & 3);
+    } else {
+      return D == 64 ? ((row >> 1) & 7) : (row & 15);
+    }
   }
 
   // Tiles go straight from HBM into LDS with global_load_lds_dwordx4: lane i of a wave
@@ -251,8 +261,8 @@ struct Fa16 {
 
   // S^T = K Q^T for the valid 32-key blocks (all of them when FULL). Ks points at the wave's keys.
   // Lane l reads key row l % 32 of each block, chunk 2 st + l / 32 (head-dim 16 st + 8 (l/32));
-  // the row's swizzle is l & 7 because every 32-key block starts at a multiple of 8. The lane's
-  // offsets are loop-invariant: KLane holds them.
+  // the row's swizzle is swz(l % 32) because every 32-key block starts at a multiple of 32. The
+  // lane's offsets are loop-invariant: KLane holds them.
   struct KLane {
     int off[D / 16];
   };
@@ -260,7 +270,7 @@ struct Fa16 {
     KLane k;
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
-      k.off[st] = (lane & 31) * D + 8 * ((2 * st + (lane >> 5)) ^ (lane & 7));
+      k.off[st] = (lane & 31) * D + 8 * ((2 * st + (lane >> 5)) ^ swz<false>(lane & 31));
     }
     return k;
   }
@@ -395,7 +405,7 @@ struct Fa16 {
   // V^T operands of one tile: va[kb][h][db] covers keys 32kb + 16h .. +15 and head-dim block db.
   // Vs points at the wave's keys. Lane l = 16 G + 4 j + q of a transpose read addresses key
   // row 4 (G/2) + j (+ 8 for the second read) at head-dim 32 db + 16 (G%2) + 4 q; the row's
-  // swizzle is 2 j (rows start at multiples of 4), so the lane's offset for block db is a
+  // swizzle is swz(j) (rows start at multiples of 4), so the lane's offset for block db is a
   // loop-invariant per-lane constant, VLane::off[db].
   using VOps = u32x4[kKB][2][kDB];
   struct VLane {
@@ -406,7 +416,7 @@ struct Fa16 {
     VLane v;
 #pragma unroll
     for (int db = 0; db < kDB; ++db) {
-      const int chunk = (4 * db + 2 * (G & 1) + (q >> 1)) ^ (2 * j);
+      const int chunk = (4 * db + 2 * (G & 1) + (q >> 1)) ^ swz<true>(j);
       v.off[db] = (4 * (G >> 1) + j) * D + 8 * chunk + 4 * (q & 1);
     }
     return v;
