@@ -1,0 +1,594 @@
+// fa_bench.hip -- torch-free benchmark of the fused attention forward through the C-ABI
+// (libfa_hip.so, include/fa/attention.h). The MI355X counterpart of the reference's fa_bench
+// (ref:bench/bench_main.cu); it writes rows of the reference's frozen CSV schema
+// (ref:CONTRACT.md:25-39) so that the same tables and scripts read both.
+//
+// Protocol (ref:bench/bench_main.cu:3-21, ref:docs/BENCHMARK_PROTOCOL.md:10-35), adapted to MI355X:
+//   * 4 rotating input sets (fewer only when memory is short; notes say `sets=<n>`), uniform in
+//     [-1, 1) from a counter-based hash on the device, one seed per tensor and set;
+//   * a 1 GiB buffer is cleared before EVERY timed launch, outside the event pair: 256 MB, the
+//     reference's size, no longer exceeds the L2 plus the 256 MB Infinity Cache of an MI355X;
+//   * one hipEvent pair per launch, one hipDeviceSynchronize after the loop;
+//   * iterations: at least --iters (100) and at least 500 ms of timed work, sized from three
+//     launches after the warmup;
+//   * median / p10 / p90 (linear interpolation between order statistics);
+//   * the output is checksummed (FNV-1a into a volatile sink) and must be finite, and a row is
+//     written only after an fp64 check of sampled rows passes: the first and last --check-rows/2
+//     query rows of heads (0, 0) and (B-1, H-1), against caps 1e-4 / 1e-2 / 5e-2 on O (fp32 /
+//     fp16 / bf16) and ten times that on LSE, the reference's sanity caps
+//     (ref:bench/bench_main.cu:603,650); the parity bar itself lives in the test suite;
+//   * the shader clock is measured on the device (s_memtime cycles over s_memrealtime at its
+//     fixed 100 MHz) right after the timed loop, in a one-workgroup probe: clock_mhz. There is no
+//     clock lock on this pool, so notes say `clock=unlocked`.
+//   * FLOPs 4*B*H*N^2*D, halved for causal (the fused stages skip masked tiles: notes
+//     `flops=causal_half`); bytes = modelled minimum Q+K+V+O+LSE (ref:bench/bench_main.cu:570-580).
+// CSV columns keep the reference's names. On this platform `nvcc` carries the HIP runtime
+// version, `ncu` the rocprofv3 version from $FA_ROCPROF_VERSION (empty when unset), `driver` the
+// HIP driver version, `torch` is blank (torch-free binary), `gpu` the device name with its gfx
+// architecture, `commit` --commit, else $FA_COMMIT, else "unknown". The binary starts no other
+// program (no git, no rocprofv3 --version): a process that has initialised the GPU must not fork
+// and exec, and under rocprofv3 the GPU is initialised before main() runs. profile.sh exports
+// both variables before it starts the binary.
+// Exit codes (ref:bench/bench_main.cu:25-26): 0 ok; 1 HIP error or failed check; 2 usage;
+// 3 stage not implemented for this (dtype, D, arch); 4 inputs do not fit in device memory.
+#include <hip/hip_runtime.h>
+#include <sys/stat.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "fa/attention.h"
+
+namespace {
+
+constexpr int kOk = 0, kError = 1, kUsage = 2, kNotImplemented = 3, kNoMemory = 4;
+constexpr std::size_t kFlushBytes = std::size_t{1} << 30;
+constexpr int kMaxSets = 4;
+constexpr double kMinTimedMs = 500.0;
+constexpr int kMaxIters = 100000;
+constexpr double kNoiseRatio = 1.5;  // p90 / p10 above this: notes say `noisy`
+constexpr const char* kCsvHeader =
+    "commit,gpu,driver,nvcc,torch,ncu,clock_mhz,impl,stage,dtype,B,H,N,D,causal,ms_median,ms_p10,"
+    "ms_p90,tflops,gbps,notes";
+
+#define HIP_OK(expr)                                                                    \
+  do {                                                                                  \
+    const hipError_t e_ = (expr);                                                       \
+    if (e_ != hipSuccess) {                                                             \
+      std::fprintf(stderr, "%s:%d: %s: %s\n", __FILE__, __LINE__, #expr,               \
+                   hipGetErrorString(e_));                                              \
+      std::exit(kError);                                                                \
+    }                                                                                   \
+  } while (0)
+
+// ---- device side: input fill and clock probe ------------------------------------------------
+// murmur3's 32-bit finaliser as a counter hash: element i of the tensor with `seed`.
+__device__ __forceinline__ uint32_t mix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x85ebca6bu;
+  x ^= x >> 13;
+  x *= 0xc2b2ae35u;
+  x ^= x >> 16;
+  return x;
+}
+
+template <typename T>
+__device__ __forceinline__ T cvt(float f) {
+  return static_cast<T>(f);
+}
+
+template <typename T>
+__global__ void fill_uniform(T* p, std::size_t n, uint32_t seed) {
+  const std::size_t stride = static_cast<std::size_t>(gridDim.x) * blockDim.x;
+  for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += stride) {
+    const uint32_t r = mix32(static_cast<uint32_t>(i) ^ mix32(seed + static_cast<uint32_t>(i >> 32)));
+    p[i] = cvt<T>(static_cast<float>(r >> 8) * (2.0f / 16777216.0f) - 1.0f);
+  }
+}
+
+// One wave spins on dependent fp32 FMAs for `iters` steps and records shader cycles and the
+// 100 MHz reference count over the same window.
+__global__ void clock_probe(unsigned long long* out, int iters, float seed) {
+  float x = seed;
+  const unsigned long long c0 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+  for (int i = 0; i < iters; ++i) x = __builtin_fmaf(x, 0.999999f, 1e-7f);
+  const unsigned long long c1 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) {
+    out[0] = c1 - c0;
+    out[1] = r1 - r0;
+    out[2] = x == 12345.f ? 1 : 0;  // keeps the chain alive
+  }
+}
+
+// ---- host helpers --------------------------------------------------------------------------
+struct Options {
+  int stage = 5;
+  std::string cfg = "C64";
+  std::string dtype = "fp16";
+  int causal = 0;
+  int iters = 100;
+  int warmup = 10;
+  bool iters_given = false;
+  std::string out;
+  std::string commit;
+  int check_rows = 64;
+  int hkv = 0;
+  float scale = 0.f;
+  bool list = false;
+  bool smoke = false;
+};
+
+void usage(FILE* f) {
+  std::fprintf(f,
+               "fa_bench --stage N [--cfg C64|C128|B2_H8_N2048_D64] [--dtype fp32|fp16|bf16]\n"
+               "         [--causal 0|1] [--iters 100] [--warmup 10] [--out path.csv]\n"
+               "         [--commit sha] [--check-rows 64] [--hkv H] [--scale s]\n"
+               "fa_bench --smoke [--stage N]   # one small launch + check, no CSV row\n"
+               "fa_bench --list                # stage x dtype x D support on this GPU\n");
+}
+
+bool parse_int(const char* s, int* v) {
+  char* end = nullptr;
+  const long x = std::strtol(s, &end, 10);
+  if (end == s || *end != '\0') return false;
+  *v = static_cast<int>(x);
+  return true;
+}
+
+int parse_args(int argc, char** argv, Options* o) {
+  for (int i = 1; i < argc; ++i) {
+    const std::string a = argv[i];
+    auto next = [&]() -> const char* { return i + 1 < argc ? argv[++i] : nullptr; };
+    if (a == "--help" || a == "-h") {
+      usage(stdout);
+      std::exit(kOk);
+    } else if (a == "--list") {
+      o->list = true;
+    } else if (a == "--smoke") {
+      o->smoke = true;
+    } else {
+      const char* v = next();
+      if (v == nullptr) return kUsage;
+      bool ok = true;
+      if (a == "--stage") ok = parse_int(v, &o->stage);
+      else if (a == "--cfg") o->cfg = v;
+      else if (a == "--dtype") o->dtype = v;
+      else if (a == "--causal") ok = parse_int(v, &o->causal);
+      else if (a == "--iters") ok = parse_int(v, &o->iters), o->iters_given = true;
+      else if (a == "--warmup") ok = parse_int(v, &o->warmup);
+      else if (a == "--out") o->out = v;
+      else if (a == "--commit") o->commit = v;
+      else if (a == "--check-rows") ok = parse_int(v, &o->check_rows);
+      else if (a == "--hkv") ok = parse_int(v, &o->hkv);
+      else if (a == "--scale") o->scale = std::strtof(v, nullptr);
+      else ok = false;
+      if (!ok) return kUsage;
+    }
+  }
+  if (o->iters < 1 || o->warmup < 0 || o->check_rows < 0) return kUsage;
+  return kOk;
+}
+
+bool parse_dtype(const std::string& s, int* dt) {
+  if (s == "fp32") return *dt = FA_DTYPE_F32, true;
+  if (s == "fp16") return *dt = FA_DTYPE_F16, true;
+  if (s == "bf16") return *dt = FA_DTYPE_BF16, true;
+  return false;
+}
+
+// C64 / C128 are the canonical profiling configs (ref:CONTRACT.md:53-56); B%d_H%d_N%d_D%d
+// otherwise.
+bool parse_cfg(const std::string& s, fa_params* p) {
+  if (s == "C64" || s == "c64") return p->B = 2, p->H = 8, p->N = 2048, p->D = 64, true;
+  if (s == "C128" || s == "c128") return p->B = 2, p->H = 8, p->N = 2048, p->D = 128, true;
+  return std::sscanf(s.c_str(), "B%d_H%d_N%d_D%d", &p->B, &p->H, &p->N, &p->D) == 4 &&
+         p->B > 0 && p->H > 0 && p->N > 0 && p->D > 0;
+}
+
+double to_double(const void* p, std::size_t i, int dt) {
+  if (dt == FA_DTYPE_F32) return static_cast<const float*>(p)[i];
+  if (dt == FA_DTYPE_F16) return static_cast<double>(static_cast<const _Float16*>(p)[i]);
+  uint32_t bits = static_cast<uint32_t>(static_cast<const uint16_t*>(p)[i]) << 16;
+  float f;
+  std::memcpy(&f, &bits, 4);
+  return f;
+}
+
+void fill(void* p, std::size_t n, int dt, uint32_t seed, hipStream_t s) {
+  if (dt == FA_DTYPE_F32) {
+    hipLaunchKernelGGL(fill_uniform<float>, dim3(2048), dim3(256), 0, s, static_cast<float*>(p), n, seed);
+  } else if (dt == FA_DTYPE_F16) {
+    hipLaunchKernelGGL(fill_uniform<_Float16>, dim3(2048), dim3(256), 0, s,
+                       static_cast<_Float16*>(p), n, seed);
+  } else {
+    hipLaunchKernelGGL(fill_uniform<__bf16>, dim3(2048), dim3(256), 0, s, static_cast<__bf16*>(p),
+                       n, seed);
+  }
+  HIP_OK(hipGetLastError());
+}
+
+struct DeviceInfo {
+  std::string name, driver, hip;
+  int arch = 0;
+  std::size_t total = 0, free = 0;
+};
+
+DeviceInfo device_info() {
+  DeviceInfo d;
+  int dev = 0;
+  HIP_OK(hipGetDevice(&dev));
+  hipDeviceProp_t prop;
+  HIP_OK(hipGetDeviceProperties(&prop, dev));
+  d.name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+  int drv = 0, rt = 0;
+  HIP_OK(hipDriverGetVersion(&drv));
+  HIP_OK(hipRuntimeGetVersion(&rt));
+  d.driver = std::to_string(drv);
+  d.hip = "hip " + std::to_string(rt / 10000000) + "." + std::to_string(rt / 100000 % 100) + "." +
+          std::to_string(rt % 100000);
+  HIP_OK(hipMemGetInfo(&d.free, &d.total));
+  if (fa_current_arch(&d.arch) != 0) d.arch = 0;
+  return d;
+}
+
+std::string env_or(const char* name, const char* fallback) {
+  const char* e = std::getenv(name);
+  return (e != nullptr && *e != '\0') ? std::string(e) : std::string(fallback);
+}
+
+std::string commit_of(const Options& o) {
+  return !o.commit.empty() ? o.commit : env_or("FA_COMMIT", "unknown");
+}
+
+std::string rocprof_version() {
+  std::string v = env_or("FA_ROCPROF_VERSION", "");
+  return v.size() > 60 ? v.substr(0, 60) : v;
+}
+
+int clock_mhz(hipStream_t s) {
+  unsigned long long* d = nullptr;
+  HIP_OK(hipMalloc(&d, 3 * sizeof(unsigned long long)));
+  hipLaunchKernelGGL(clock_probe, dim3(1), dim3(64), 0, s, d, 1 << 20, 1.0f);
+  HIP_OK(hipGetLastError());
+  unsigned long long h[3] = {0, 0, 0};
+  HIP_OK(hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, s));
+  HIP_OK(hipStreamSynchronize(s));
+  HIP_OK(hipFree(d));
+  return h[1] > 0 ? static_cast<int>(std::lround(static_cast<double>(h[0]) / h[1] * 100.0)) : 0;
+}
+
+double quantile(const std::vector<float>& sorted, double q) {
+  const double pos = q * static_cast<double>(sorted.size() - 1);
+  const std::size_t lo = static_cast<std::size_t>(pos);
+  const std::size_t hi = std::min(lo + 1, sorted.size() - 1);
+  return sorted[lo] + (pos - static_cast<double>(lo)) * (sorted[hi] - sorted[lo]);
+}
+
+volatile uint64_t g_sink = 0;
+
+uint64_t fnv1a(const std::vector<uint8_t>& b) {
+  uint64_t h = 0xcbf29ce484222325ull;
+  for (uint8_t c : b) h = (h ^ c) * 0x100000001b3ull;
+  return h;
+}
+
+std::string fmt(const char* f, double v) {
+  char buf[64];
+  std::snprintf(buf, sizeof(buf), f, v);
+  return buf;
+}
+
+std::string csv_field(const std::string& s) {
+  if (s.find_first_of(",\"\n") == std::string::npos) return s;
+  std::string q = "\"";
+  for (char c : s) q += c == '"' ? std::string("\"\"") : std::string(1, c);
+  return q + "\"";
+}
+
+void mkdir_parents(const std::string& path) {
+  for (std::size_t i = 1; i < path.size(); ++i) {
+    if (path[i] == '/') mkdir(path.substr(0, i).c_str(), 0755);
+  }
+}
+
+// Prints header + row, and appends the row to --out (header first when the file is new).
+bool emit(const std::vector<std::string>& cols, const std::string& out) {
+  std::string line;
+  for (std::size_t i = 0; i < cols.size(); ++i) line += (i ? "," : "") + cols[i];
+  std::printf("%s\n%s\n", kCsvHeader, line.c_str());
+  if (out.empty()) return true;
+  mkdir_parents(out);
+  long size = 0;
+  if (FILE* f = std::fopen(out.c_str(), "r")) {
+    std::fseek(f, 0, SEEK_END);
+    size = std::ftell(f);
+    std::fclose(f);
+  }
+  FILE* f = std::fopen(out.c_str(), "a");
+  if (f == nullptr) {
+    std::fprintf(stderr, "cannot open %s for append\n", out.c_str());
+    return false;
+  }
+  if (size <= 0) std::fprintf(f, "%s\n", kCsvHeader);
+  std::fprintf(f, "%s\n", line.c_str());
+  std::fclose(f);
+  std::printf("appended to %s\n", out.c_str());
+  return true;
+}
+
+// fp64 attention of query rows [r0, r0 + nr) of one head against all keys (top-left causal),
+// O and LSE = m*scale + ln(sum): the sanity check of this harness.
+void rows_fp64(const std::vector<double>& q, const std::vector<double>& k,
+               const std::vector<double>& v, int N, int D, double scale, bool causal, int r0,
+               int nr, std::vector<double>* o, std::vector<double>* lse) {
+  std::vector<double> s(N);
+  for (int i = 0; i < nr; ++i) {
+    const int row = r0 + i;
+    const int kend = causal ? row + 1 : N;
+    double m = -INFINITY;
+    for (int j = 0; j < kend; ++j) {
+      double d = 0;
+      for (int x = 0; x < D; ++x) d += q[static_cast<std::size_t>(i) * D + x] * k[static_cast<std::size_t>(j) * D + x];
+      s[j] = d * scale;
+      m = std::max(m, s[j]);
+    }
+    double l = 0;
+    for (int j = 0; j < kend; ++j) l += (s[j] = std::exp(s[j] - m));
+    for (int x = 0; x < D; ++x) {
+      double acc = 0;
+      for (int j = 0; j < kend; ++j) acc += s[j] * v[static_cast<std::size_t>(j) * D + x];
+      (*o)[static_cast<std::size_t>(i) * D + x] = acc / l;
+    }
+    (*lse)[i] = m + std::log(l);
+  }
+}
+
+bool self_check(const fa_params& p, int dt, const void* dq, const void* dk, const void* dv,
+                const void* dO, const float* dlse, int rows, int* checked) {
+  const std::size_t es = fa_dtype_size(dt);
+  const std::size_t nd = static_cast<std::size_t>(p.N) * p.D;
+  std::vector<std::pair<int, int>> ranges;
+  if (p.N <= rows) {
+    ranges.emplace_back(0, p.N);
+  } else {
+    const int half = std::max(1, rows / 2);
+    ranges.emplace_back(0, half);
+    ranges.emplace_back(p.N - half, half);
+  }
+  std::vector<std::pair<int, int>> heads = {{0, 0}};
+  if (p.B > 1 || p.H > 1) heads.emplace_back(p.B - 1, p.H - 1);
+  const double cap = dt == FA_DTYPE_F32 ? 1e-4 : dt == FA_DTYPE_F16 ? 1e-2 : 5e-2;
+  double err_o = 0, err_l = 0;
+  *checked = 0;
+  std::vector<uint8_t> hk(nd * es), hv(nd * es);
+  std::vector<double> k(nd), v(nd);
+  for (const auto& [b, h] : heads) {
+    const int hk_idx = h / (p.H / p.Hkv);
+    const std::size_t kv_off = (static_cast<std::size_t>(b) * p.Hkv + hk_idx) * nd * es;
+    HIP_OK(hipMemcpy(hk.data(), static_cast<const uint8_t*>(dk) + kv_off, hk.size(), hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(hv.data(), static_cast<const uint8_t*>(dv) + kv_off, hv.size(), hipMemcpyDeviceToHost));
+    for (std::size_t i = 0; i < nd; ++i) k[i] = to_double(hk.data(), i, dt), v[i] = to_double(hv.data(), i, dt);
+    for (const auto& [r0, nr] : ranges) {
+      const std::size_t rd = static_cast<std::size_t>(nr) * p.D;
+      const std::size_t q_off = ((static_cast<std::size_t>(b) * p.H + h) * p.N + r0) * p.D * es;
+      const std::size_t l_off = (static_cast<std::size_t>(b) * p.H + h) * p.N + r0;
+      std::vector<uint8_t> hq(rd * es), ho(rd * es);
+      std::vector<float> hl(nr);
+      HIP_OK(hipMemcpy(hq.data(), static_cast<const uint8_t*>(dq) + q_off, hq.size(), hipMemcpyDeviceToHost));
+      HIP_OK(hipMemcpy(ho.data(), static_cast<const uint8_t*>(dO) + q_off, ho.size(), hipMemcpyDeviceToHost));
+      HIP_OK(hipMemcpy(hl.data(), dlse + l_off, hl.size() * 4, hipMemcpyDeviceToHost));
+      std::vector<double> q(rd), o_ref(rd), l_ref(nr);
+      for (std::size_t i = 0; i < rd; ++i) q[i] = to_double(hq.data(), i, dt);
+      rows_fp64(q, k, v, p.N, p.D, p.scale, p.causal, r0, nr, &o_ref, &l_ref);
+      for (std::size_t i = 0; i < rd; ++i) err_o = std::max(err_o, std::fabs(to_double(ho.data(), i, dt) - o_ref[i]));
+      for (int i = 0; i < nr; ++i) err_l = std::max(err_l, std::fabs(hl[i] - l_ref[i]));
+      *checked += nr;
+    }
+  }
+  const bool ok = err_o <= cap && err_l <= 10 * cap;
+  std::printf("%s rows=%d heads=%zu max_abs_err_o=%.3g (cap %.0e) max_abs_err_lse=%.3g\n",
+              ok ? "CHECK_OK" : "CHECK_FAIL", *checked, heads.size(), err_o, cap, err_l);
+  return ok;
+}
+
+int list_support(const DeviceInfo& dev) {
+  std::printf("device %s arch %d\n", dev.name.c_str(), dev.arch);
+  for (int st = 1; st <= 5; ++st) {
+    for (int dt = 0; dt < 3; ++dt) {
+      for (int D : {64, 128}) {
+        std::printf("stage %d %-6s %-5s D=%3d : %s\n", st, fa_impl_name(st), fa_dtype_name(dt), D,
+                    fa_impl_supports(st, dt, D, dev.arch) ? "yes" : "no");
+      }
+    }
+  }
+  return kOk;
+}
+
+int run(const Options& opt, const DeviceInfo& dev, hipStream_t stream) {
+  fa_params p{};
+  int dt = 0;
+  const std::string cfg = opt.smoke ? std::string("B1_H2_N256_D64") : opt.cfg;
+  if (!parse_cfg(cfg, &p) || !parse_dtype(opt.dtype, &dt)) {
+    std::fprintf(stderr, "bad --cfg '%s' or --dtype '%s'\n", cfg.c_str(), opt.dtype.c_str());
+    return kUsage;
+  }
+  if (opt.stage < 1 || opt.stage > 5) {
+    std::fprintf(stderr, "--stage must be 1..5\n");
+    return kUsage;
+  }
+  p.Hkv = opt.hkv > 0 ? opt.hkv : p.H;
+  p.causal = opt.causal != 0;
+  p.scale = opt.scale > 0.f ? opt.scale : 1.0f / std::sqrt(static_cast<float>(p.D));
+  if (!fa_impl_supports(opt.stage, dt, p.D, dev.arch)) {
+    std::printf("stage %d not implemented (%s/%s D=%d on gfx%d)\n", opt.stage,
+                fa_impl_name(opt.stage), fa_dtype_name(dt), p.D, dev.arch);
+    return kNotImplemented;
+  }
+  const std::size_t es = fa_dtype_size(dt);
+  const std::size_t q_bytes = static_cast<std::size_t>(p.B) * p.H * p.N * p.D * es;
+  const std::size_t kv_bytes = static_cast<std::size_t>(p.B) * p.Hkv * p.N * p.D * es;
+  const std::size_t lse_bytes = static_cast<std::size_t>(p.B) * p.H * p.N * sizeof(float);
+  const std::size_t ws_bytes = fa_workspace_bytes(opt.stage, dt, &p);
+  const std::size_t set_bytes = q_bytes + 2 * kv_bytes;
+  const std::size_t fixed = q_bytes + lse_bytes + ws_bytes + kFlushBytes;
+  const std::size_t budget = dev.free - dev.free / 10;
+  int nsets = kMaxSets;
+  while (nsets > 1 && fixed + static_cast<std::size_t>(nsets) * set_bytes > budget) --nsets;
+  if (fixed + set_bytes > budget) {
+    std::fprintf(stderr, "inputs do not fit: need %.2f GB, budget %.2f GB\n",
+                 (fixed + set_bytes) / 1e9, budget / 1e9);
+    return kNoMemory;
+  }
+  std::vector<std::string> notes;
+  if (opt.smoke) notes.push_back("smoke");
+  if (p.causal) notes.push_back("flops=causal_half");
+  if (p.Hkv != p.H) notes.push_back("hkv=" + std::to_string(p.Hkv));
+  if (nsets < kMaxSets) notes.push_back("sets=" + std::to_string(nsets));
+
+  std::vector<void*> q(nsets), k(nsets), v(nsets);
+  for (int s = 0; s < nsets; ++s) {
+    HIP_OK(hipMalloc(&q[s], q_bytes));
+    HIP_OK(hipMalloc(&k[s], kv_bytes));
+    HIP_OK(hipMalloc(&v[s], kv_bytes));
+    fill(q[s], q_bytes / es, dt, 0x9e37u * (s + 1) + 11, stream);
+    fill(k[s], kv_bytes / es, dt, 0x9e37u * (s + 1) + 23, stream);
+    fill(v[s], kv_bytes / es, dt, 0x9e37u * (s + 1) + 37, stream);
+  }
+  void *o = nullptr, *ws = nullptr, *flush = nullptr;
+  float* lse = nullptr;
+  HIP_OK(hipMalloc(&o, q_bytes));
+  HIP_OK(hipMalloc(reinterpret_cast<void**>(&lse), lse_bytes));
+  if (ws_bytes > 0) HIP_OK(hipMalloc(&ws, ws_bytes));
+  HIP_OK(hipMalloc(&flush, kFlushBytes));
+  auto launch = [&](int s) {
+    return fa_forward(opt.stage, dt, q[s], k[s], v[s], o, lse, ws, &p, stream);
+  };
+
+  int err = launch(0);
+  if (err == hipSuccess) err = hipStreamSynchronize(stream);
+  if (err != hipSuccess) {
+    std::fprintf(stderr, "fa_forward failed: %s\n", fa_error_string(err));
+    return kError;
+  }
+  if (opt.check_rows > 0) {
+    int checked = 0;
+    if (!self_check(p, dt, q[0], k[0], v[0], o, lse, opt.check_rows, &checked)) return kError;
+    notes.push_back("check=rows" + std::to_string(checked));
+  }
+  std::vector<uint8_t> host_o(q_bytes);
+  HIP_OK(hipMemcpy(host_o.data(), o, q_bytes, hipMemcpyDeviceToHost));
+  std::size_t nonfinite = 0;
+  for (std::size_t i = 0; i < q_bytes / es; ++i) nonfinite += std::isfinite(to_double(host_o.data(), i, dt)) ? 0 : 1;
+  if (nonfinite > 0) {
+    std::fprintf(stderr, "CHECK_FAIL nonfinite=%zu output elements\n", nonfinite);
+    return kError;
+  }
+  g_sink = fnv1a(host_o);
+  std::printf("checksum=%016llx\n", static_cast<unsigned long long>(g_sink));
+
+  // Timed loop: warmup, then (unless --iters was given) size the count from three launches.
+  const int warmup = opt.smoke ? 1 : opt.warmup;
+  for (int w = 0; w < warmup; ++w) {
+    HIP_OK(hipMemsetAsync(flush, 0, kFlushBytes, stream));
+    if ((err = launch(w % nsets)) != hipSuccess) break;
+  }
+  int iters = opt.smoke ? 3 : opt.iters;
+  hipEvent_t a = nullptr, b = nullptr;
+  HIP_OK(hipEventCreate(&a));
+  HIP_OK(hipEventCreate(&b));
+  if (err == hipSuccess && !opt.smoke && !opt.iters_given) {
+    HIP_OK(hipEventRecord(a, stream));
+    for (int i = 0; i < 3 && err == hipSuccess; ++i) err = launch(i % nsets);
+    HIP_OK(hipEventRecord(b, stream));
+    HIP_OK(hipEventSynchronize(b));
+    float est = 0.f;
+    HIP_OK(hipEventElapsedTime(&est, a, b));
+    const double per = std::max(static_cast<double>(est) / 3.0, 1e-3);
+    iters = std::max(iters, std::min(kMaxIters, static_cast<int>(std::ceil(kMinTimedMs / per))));
+  }
+  std::vector<hipEvent_t> ev(2 * static_cast<std::size_t>(iters));
+  for (hipEvent_t& e : ev) HIP_OK(hipEventCreate(&e));
+  for (int i = 0; i < iters && err == hipSuccess; ++i) {
+    HIP_OK(hipMemsetAsync(flush, 0, kFlushBytes, stream));  // cache eviction, untimed
+    HIP_OK(hipEventRecord(ev[2 * i], stream));
+    err = launch(i % nsets);
+    HIP_OK(hipEventRecord(ev[2 * i + 1], stream));
+  }
+  if (err == hipSuccess) err = hipDeviceSynchronize();
+  if (err != hipSuccess) {
+    std::fprintf(stderr, "timed loop failed: %s\n", fa_error_string(err));
+    return kError;
+  }
+  std::vector<float> ms(iters);
+  for (int i = 0; i < iters; ++i) HIP_OK(hipEventElapsedTime(&ms[i], ev[2 * i], ev[2 * i + 1]));
+  for (hipEvent_t e : ev) HIP_OK(hipEventDestroy(e));
+  HIP_OK(hipEventDestroy(a));
+  HIP_OK(hipEventDestroy(b));
+  const int mhz = clock_mhz(stream);
+  std::sort(ms.begin(), ms.end());
+  const double med = quantile(ms, 0.5), p10 = quantile(ms, 0.1), p90 = quantile(ms, 0.9);
+  notes.push_back("clock=unlocked");
+  notes.push_back("iters=" + std::to_string(iters));
+  notes.push_back("warmup=" + std::to_string(warmup));
+  notes.push_back("flush=1GiB");
+  if (p10 > 0 && p90 / p10 >= kNoiseRatio) notes.push_back("noisy");
+  const double flops = 4.0 * p.B * p.H * static_cast<double>(p.N) * p.N * p.D * (p.causal ? 0.5 : 1.0);
+  const double bytes = 2.0 * q_bytes + 2.0 * kv_bytes + lse_bytes;
+  const double tflops = flops / (med * 1e-3) / 1e12, gbps = bytes / (med * 1e-3) / 1e9;
+  std::printf("stage %d %s %s %s causal=%d: median %.4f ms (p10 %.4f, p90 %.4f, min %.4f, max %.4f) "
+              "over %d iters/%d warmup/%d sets -> %.3f TFLOP/s, %.1f GB/s, clock %d MHz\n",
+              opt.stage, fa_impl_name(opt.stage), cfg.c_str(), fa_dtype_name(dt), p.causal ? 1 : 0,
+              med, p10, p90, ms.front(), ms.back(), iters, warmup, nsets, tflops, gbps, mhz);
+
+  std::string joined;
+  for (std::size_t i = 0; i < notes.size(); ++i) joined += (i ? ";" : "") + notes[i];
+  const std::vector<std::string> cols = {
+      csv_field(commit_of(opt)), csv_field(dev.name), csv_field(dev.driver), csv_field(dev.hip), "",
+      csv_field(rocprof_version()), std::to_string(mhz), fa_impl_name(opt.stage),
+      std::to_string(opt.stage), fa_dtype_name(dt), std::to_string(p.B), std::to_string(p.H),
+      std::to_string(p.N), std::to_string(p.D), std::to_string(p.causal ? 1 : 0), fmt("%.4f", med),
+      fmt("%.4f", p10), fmt("%.4f", p90), fmt("%.3f", tflops), fmt("%.1f", gbps), csv_field(joined)};
+  const bool ok = opt.smoke ? true : emit(cols, opt.out);
+  for (int s = 0; s < nsets; ++s) {
+    HIP_OK(hipFree(q[s]));
+    HIP_OK(hipFree(k[s]));
+    HIP_OK(hipFree(v[s]));
+  }
+  HIP_OK(hipFree(o));
+  HIP_OK(hipFree(lse));
+  HIP_OK(hipFree(flush));
+  if (ws != nullptr) HIP_OK(hipFree(ws));
+  return ok ? kOk : kError;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  Options opt;
+  if (parse_args(argc, argv, &opt) != kOk) {
+    usage(stderr);
+    return kUsage;
+  }
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+    std::fprintf(stderr, "no HIP device\n");
+    return kError;
+  }
+  const DeviceInfo dev = device_info();
+  if (opt.list) return list_support(dev);
+  hipStream_t stream = nullptr;
+  HIP_OK(hipStreamCreate(&stream));
+  const int rc = run(opt, dev, stream);
+  HIP_OK(hipStreamDestroy(stream));
+  return rc;
+}

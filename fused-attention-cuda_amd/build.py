@@ -4,6 +4,7 @@
   libfa_hip.so  hipcc --offload-arch=gfx950: csrc/dispatch.cpp + csrc/attn_{f16,bf16,f32}.hip.
                 Exports exactly the functions of include/fa/attention.h.
   _C.so         csrc/ext.cpp against PyTorch-ROCm, linked to libfa_hip.so (rpath $ORIGIN).
+  bench/fa_bench  the torch-free benchmark binary (bench/fa_bench.hip), linked to libfa_hip.so.
 
 Both land in fused-attention-cuda_amd/fused_attn/, next to the Python package that loads them.
 Object files go to fused-attention-cuda_amd/_build/. Every call rebuilds everything (the build
@@ -96,6 +97,13 @@ def build(jobs: int = 8) -> None:
          *map(str, host_objs), *map(str, hip_objs), "-Wl,-soname,libfa_hip.so"])
     os.replace(tmp, lib)
 
+    bench_src = PKG_ROOT / "bench" / "fa_bench.hip"
+    bench_bin = PKG_ROOT / "bench" / "fa_bench"
+    tmp = bench_bin.with_suffix(".tmp")
+    run([HIPCC, *HIP_FLAGS, str(bench_src), "-o", str(tmp), f"-L{OUT}", "-lfa_hip",
+         "-Wl,-rpath,$ORIGIN/../fused_attn"])
+    os.replace(tmp, bench_bin)
+
     cflags, ldflags = torch_flags()
     ext_obj = BUILD / "ext.cpp.o"
     run(["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-parameter",
@@ -114,7 +122,7 @@ def main() -> int:
     ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
     a = ap.parse_args()
     build(a.jobs)
-    print(f"built {OUT / 'libfa_hip.so'} and {OUT / '_C.so'}")
+    print(f"built {OUT / 'libfa_hip.so'}, {OUT / '_C.so'} and {PKG_ROOT / 'bench' / 'fa_bench'}")
     return 0
 
 
