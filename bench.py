@@ -219,6 +219,39 @@ def bench_workload(torch, capi, name, stage, steps, warmup, seed=0, gate_it=True
     return res, sets, stream, causal, scale
 
 
+def decode_line(torch):
+    """Split-KV decode (fa_decode): one new token per sequence against a bf16 KV cache,
+    B8 H32 Hkv8 Nkv8192 D128 (a GQA 4:1 model at 8K context). The kernel is HBM-bound: its
+    algorithmic bytes are K + V of the cache plus q and o (the partials stay in the L2/MALL-sized
+    workspace), reported against MI355X's 8 TB/s. Timed like the forward: 4 rotating input sets,
+    back to back, one event pair around the loop on the launch stream."""
+    import fused_attn
+
+    b, h, hkv, nq, nkv, d = 8, 32, 8, 1, 8192, 128
+    dt = torch.bfloat16
+    gen = torch.Generator(device="cpu").manual_seed(7)
+    sets = [tuple(torch.randn(*shape, generator=gen).to("cuda", dt)
+                  for shape in ((b, h, nq, d), (b, hkv, nkv, d), (b, hkv, nkv, d)))
+            for _ in range(4)]
+    for i in range(20):
+        fused_attn.decode(*sets[i % 4], is_causal=True)
+    torch.cuda.synchronize()
+    iters = 200
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(iters):
+        fused_attn.decode(*sets[i % 4], is_causal=True)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    nbytes = 2 * b * hkv * nkv * d * 2 + 2 * b * h * nq * d * 2 + b * h * nq * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"config": f"B{b} H{h} Hkv{hkv} Nq{nq} Nkv{nkv} D{d} bf16 causal (bottom-right)",
+            "ms": round(ms, 6), "algorithmic_bytes": nbytes, "GB_per_s": round(gbs, 1),
+            "roofline": {"bound": "hbm", "peak": 8000.0, "unit": "GB/s",
+                         "frac": round(gbs / 8000.0, 4)}}
+
+
 def gpt_block_line(torch):
     """one GPT-2-small decoder block (768 wide, 12 heads of 64, T 1024, batch 8,
     fp16, causal, random init, random token ids through a wte/wpe embedding), tokens/s with the
@@ -328,6 +361,7 @@ def main(argv=None) -> int:
                             for kk, vv in res.items()}
         line["configs"] = others
         line["gpt_block"] = gpt_block_line(torch)
+        line["decode"] = decode_line(torch)
     print(json.dumps(line))
     return 0
 

@@ -1,0 +1,292 @@
+// attn_decode.h -- split-KV decode (flash-decoding) for 16-bit operands on gfx950: Nq new query
+// tokens per sequence attend to Nkv cached keys, with the key range cut into splits that run in
+// parallel, each writing a partial (O, LSE); a second kernel combines the splits with LSE weights.
+// The reference lists this as its next component (ref:README.md:1357-1358) and emits LSE for it
+// (ref:include/fa/softmax_math.cuh:65-68); the algorithm is the one its research notes give
+// (ref:docs/RESEARCH.md:151-156): O = sum_s e^(L_s - L*) O_s / sum_s e^(L_s - L*), L* = max_s L_s.
+//
+// Included by attn_f16.hip and attn_bf16.hip. Kernel entry points:
+//   fa_decode_split<T, D>    one workgroup per (split, kv head, batch); 4 waves
+//   fa_decode_combine<T, D>  one wave per (batch, head, query token)
+//
+// Work decomposition. The G = H / Hkv query heads of one kv head, times the Nq query tokens, are
+// R = G * Nq rows that read the same keys; in q ([B, H, Nq, D]) they are contiguous (head-major,
+// then token), so they form one 32-row MFMA tile (R <= 32 is required; rows past R are zero).
+// Keys stream through LDS in tiles of 128 (LDS-DMA, two buffers, the next tile in flight while
+// the current one is used); wave w takes keys [32 w, 32 w + 32) of every tile, and the four
+// partial (m, l, O) are merged through LDS at the end (the stage-5 machinery with RG = 1, KS = 4).
+// Masking is per lane: row r is query token i = r % Nq, which sees keys j <= Nkv - Nq + i when
+// causal (bottom-right: the new tokens are the last Nq positions) and j <= Nkv - 1 otherwise.
+// Split boundaries are multiples of 128 keys, so only the last split has a ragged end.
+//
+// The kernel is bound by HBM reads of K and V (2 Nkv D bytes per element type and kv head).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "attn_mfma16.h"
+#include "fa_internal.h"
+
+namespace fa {
+namespace m16 {
+
+// One LDS-DMA wave instruction issued as inline asm: lane i copies 16 bytes from `src` to LDS
+// byte offset lds + 16 i. Hidden from the compiler, the DMA of the next tile does not make the
+// LDS reads of the current tile wait for it (the builtin form would put a vmcnt(0) in front of
+// them); the kernel waits itself (vmcnt(0) before the barrier that publishes the tile). M0 is an
+// output of the statement, so the compiler knows it is overwritten.
+__device__ __forceinline__ void dec_dma16(const void* src, uint32_t lds) {
+  uint32_t m0;
+  asm volatile("s_mov_b32 %0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               : "={m0}"(m0)
+               : "v"(src), "s"(lds)
+               : "memory");
+}
+
+template <typename T, int D>
+struct Dec16 {
+  using F = Fa16<T, D, 1, 4, 32, true>;  // 32 rows, 4 key-split waves of 32 keys, 2 buffers
+  static constexpr int BC = F::BC;        // 128 keys per tile
+  static constexpr int kWaves = F::kWaves;
+  static constexpr int kThreads = F::kThreads;
+  static constexpr int kKB = F::kKB;  // 1
+  static constexpr int kDB = F::kDB;
+
+  // The tile of keys [k0, k0 + BC) of one tensor into `buf` through dec_dma16; rows past the
+  // range read its last row (N - 1), inside the tensor, and are masked by the math.
+  template <bool IS_V>
+  __device__ static void dma_tile(T* buf, const T* gbase, const typename F::Dma& d, int k0, int N,
+                                  int wave) {
+    const T* tile = gbase + static_cast<ptrdiff_t>(k0) * D;
+#pragma unroll
+    for (int i = 0; i < F::kDmaPerWave; ++i) {
+      const int last = min(d.row[i], N - 1 - k0);
+      dec_dma16(tile + d.off[i] + (last - d.row[i]) * D,
+                static_cast<uint32_t>(reinterpret_cast<uintptr_t>(buf + 512 * (wave + i * kWaves))));
+    }
+  }
+
+  __device__ static void run(const DecArgs& a) {
+    __shared__ __attribute__((aligned(16))) char lds_raw[F::kLdsBytes];
+    T* lds = reinterpret_cast<T*>(lds_raw);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 5;
+    const int s = blockIdx.x % a.S;
+    const int bh = blockIdx.x / a.S;
+    const int hkv = bh % a.Hkv;
+    const int b = bh / a.Hkv;
+    const int k_begin = s * a.chunk;
+    const int k_end = min(a.Nkv, k_begin + a.chunk);
+    const int nk = k_end - k_begin;  // >= 1: the launcher only makes non-empty splits
+    const int row = lane & 31;
+    const bool row_valid = row < a.R;
+    const int q0 = (b * a.H + hkv * a.G) * a.Nq;  // first query row of the group in q / o
+    const float c = a.c;
+
+    typename F::WaveState ws;
+    const T* qrow = static_cast<const T*>(a.q) + static_cast<size_t>(q0 + row) * D;
+#pragma unroll
+    for (int st = 0; st < D / 16; ++st) {
+      ws.q[st] = row_valid ? *reinterpret_cast<const u32x4*>(qrow + 16 * st + 8 * g)
+                           : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) ws.o[db] = f32x16{};
+    ws.m = -__builtin_inff();
+    ws.mc = 0.f;
+    ws.l = 0.f;
+    // Last visible key of this lane's row, relative to k_begin.
+    const int tok = row % a.Nq;
+    const int lim = (a.causal ? a.Nkv - a.Nq + tok : a.Nkv - 1) - k_begin;
+
+    const T* kg = static_cast<const T*>(a.k) + static_cast<size_t>(b * a.Hkv + hkv) * a.Nkv * D +
+                  static_cast<size_t>(k_begin) * D;
+    const T* vg = static_cast<const T*>(a.v) + static_cast<size_t>(b * a.Hkv + hkv) * a.Nkv * D +
+                  static_cast<size_t>(k_begin) * D;
+    T* const kbuf0 = lds;
+    T* const vbuf0 = lds + 2 * F::kKElems;
+    const int kbase = wave * 32;  // this wave's keys inside every tile
+    const typename F::KLane kl = F::k_lane(lane);
+    const typename F::VLane vl = F::v_lane(lane);
+    const typename F::Dma dk = F::template dma_lane<false>(wave, lane, D);
+    const typename F::Dma dv = F::template dma_lane<true>(wave, lane, D);
+    const int n_tiles = (nk + BC - 1) / BC;
+
+    dma_tile<false>(kbuf0, kg, dk, 0, nk, wave);
+    dma_tile<true>(vbuf0, vg, dv, 0, nk, wave);
+    F::wait_dma();
+    __syncthreads();
+    typename F::Probs P;
+    f32x16 sc[kKB];
+    for (int t = 0; t < n_tiles; ++t) {
+      const int buf = t & 1;
+      if (t + 1 < n_tiles) {  // the next tile into the other buffer (read in step t-1)
+        dma_tile<false>(kbuf0 + (buf ^ 1) * F::kKElems, kg, dk, (t + 1) * BC, nk, wave);
+        dma_tile<true>(vbuf0 + (buf ^ 1) * F::kVElems, vg, dv, (t + 1) * BC, nk, wave);
+      }
+      const int k0 = t * BC + kbase;  // this wave's first key, relative to k_begin
+      const int nv = max(0, min(kKB, (nk - k0 + 31) / 32));
+      if (nv > 0) {
+        const T* ks = kbuf0 + buf * F::kKElems + kbase * D;
+        const T* vs = vbuf0 + buf * F::kVElems + kbase * D;
+        F::template qk<false>(sc, ws, ks, nv, kl);
+        // Per-lane key limit (causal end of the row, or the ragged end of the keys): a select,
+        // not a conditional store, so the scores stay in registers.
+#pragma unroll
+        for (int kb = 0; kb < kKB; ++kb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3);
+            sc[kb][r] = key > lim ? -__builtin_inff() : sc[kb][r];
+          }
+        }
+        float mx = 0.f;
+        const float rs = F::template softmax_exp<false>(ws, sc, P, mx, nv, -1, c, lane);
+        F::template softmax_settle<false>(ws, sc, P, rs, mx, nv, -1, c);
+        F::template pv<false>(ws, P, vs, vl, nv, -1);
+      }
+      F::wait_dma();
+      __syncthreads();
+    }
+
+    // Merge the four waves' partial states of the rows (LDS is free after the last barrier).
+    float* mg = reinterpret_cast<float*>(lds_raw);
+    if (wave > 0) {
+      float* dst = mg + (wave - 1) * F::kMergeFloats;
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dst[(db * 16 + r) * 64 + lane] = ws.o[db][r];
+      }
+      dst[kDB * 16 * 64 + lane] = ws.m;
+      dst[(kDB * 16 + 1) * 64 + lane] = ws.l;
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int sp = 1; sp < kWaves; ++sp) {
+      const float* src = mg + (sp - 1) * F::kMergeFloats;
+      const float m1 = src[kDB * 16 * 64 + lane];
+      const float l1 = src[(kDB * 16 + 1) * 64 + lane];
+      const float m_new = fmaxf(ws.m, m1);
+      const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
+      const float a0 = exp2_hw((ws.m - m_use) * c);
+      const float a1 = exp2_hw((m1 - m_use) * c);
+      ws.l = ws.l * a0 + l1 * a1;
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ws.o[db][r] = ws.o[db][r] * a0 + src[(db * 16 + r) * 64 + lane] * a1;
+      }
+      ws.m = m_new;
+    }
+    const float lt = ws.l + __shfl_xor(ws.l, 32);
+    if (!row_valid) return;
+    const bool empty = !(lt > 0.f) || ws.m == -__builtin_inff();
+    const float inv = empty ? 0.f : 1.f / lt;
+    // lse of the split: m*scale + ln(l); an empty split reports -inf so the combine ignores it,
+    // and with a single split the final convention (+inf for a row with no key) applies.
+    const float lse = empty ? (a.S == 1 ? __builtin_inff() : -__builtin_inff())
+                            : ws.m * a.scale + log2_hw(lt) * kLn2;
+    if (a.S == 1) {
+      T* orow = static_cast<T*>(a.o) + static_cast<size_t>(q0 + row) * D;
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d = 32 * db + 8 * j + 4 * g;
+          const float x0 = ws.o[db][4 * j + 0] * inv, x1 = ws.o[db][4 * j + 1] * inv;
+          const float x2 = ws.o[db][4 * j + 2] * inv, x3 = ws.o[db][4 * j + 3] * inv;
+          if constexpr (F::kF16) {
+            *reinterpret_cast<f16x4*>(orow + d) = f16x4{(_Float16)x0, (_Float16)x1, (_Float16)x2, (_Float16)x3};
+          } else {
+            *reinterpret_cast<bf16x4*>(orow + d) = bf16x4{(__bf16)x0, (__bf16)x1, (__bf16)x2, (__bf16)x3};
+          }
+        }
+      }
+      if (g == 0) a.lse[q0 + row] = lse;
+    } else {
+      // Partials: o_part [B, Hkv, S, R, D] and lse_part [B, Hkv, S, R], fp32.
+      const size_t pr = (static_cast<size_t>(b * a.Hkv + hkv) * a.S + s) * a.R + row;
+      float* orow = a.o_part + pr * D;
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d = 32 * db + 8 * j + 4 * g;
+          *reinterpret_cast<float4*>(orow + d) =
+              float4{ws.o[db][4 * j] * inv, ws.o[db][4 * j + 1] * inv, ws.o[db][4 * j + 2] * inv,
+                     ws.o[db][4 * j + 3] * inv};
+        }
+      }
+      if (g == 0) a.lse_part[pr] = lse;
+    }
+  }
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void fa_decode_split(DecArgs a) {
+  Dec16<T, D>::run(a);
+}
+
+// One wave per output row (b, h, i): the LSE-weighted sum of the S partial rows. Lane l owns
+// head-dim elements [D/64 * l, D/64 * (l + 1)). lse = L* + ln(sum_s e^(L_s - L*)); a row whose
+// splits are all empty gets O = 0 and lse = +inf (the non-split convention,
+// ref:include/fa/softmax_math.cuh:62-68).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void fa_decode_combine(DecArgs a) {
+  constexpr int kPer = D / 64;
+  const int lane = threadIdx.x & 63;
+  const int orow = blockIdx.x * 4 + (threadIdx.x >> 6);  // (b, h, i) flattened
+  const int n_rows = a.B * a.H * a.Nq;
+  if (orow >= n_rows) return;
+  const int i = orow % a.Nq;
+  const int bh = orow / a.Nq;
+  const int h = bh % a.H;
+  const int b = bh / a.H;
+  const int hkv = h / a.G;
+  const int r = (h - hkv * a.G) * a.Nq + i;
+  const size_t base = static_cast<size_t>(b * a.Hkv + hkv) * a.S * a.R + r;  // split 0
+  float mx = -__builtin_inff();
+  for (int s = 0; s < a.S; ++s) mx = fmaxf(mx, a.lse_part[base + static_cast<size_t>(s) * a.R]);
+  float acc[kPer];
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) acc[e] = 0.f;
+  float wsum = 0.f;
+  if (mx != -__builtin_inff()) {
+    for (int s = 0; s < a.S; ++s) {
+      const size_t pr = base + static_cast<size_t>(s) * a.R;
+      const float w = __expf(a.lse_part[pr] - mx);
+      wsum += w;
+      const float* src = a.o_part + pr * D + kPer * lane;
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) acc[e] += w * src[e];
+    }
+  }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  T* dst = static_cast<T*>(a.o) + static_cast<size_t>(orow) * D + kPer * lane;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) dst[e] = static_cast<T>(acc[e] * inv);
+  if (lane == 0) a.lse[orow] = wsum > 0.f ? mx + __logf(wsum) : __builtin_inff();
+}
+
+template <typename T, int D>
+int launch_decode(const DecArgs& a, hipStream_t stream) {
+  const long long grid = static_cast<long long>(a.S) * a.B * a.Hkv;
+  if (grid <= 0 || grid > 0x7fffffffLL) return static_cast<int>(hipErrorInvalidValue);
+  hipLaunchKernelGGL((fa_decode_split<T, D>), dim3(static_cast<unsigned>(grid)),
+                     dim3(Dec16<T, D>::kThreads), 0, stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.S == 1) return static_cast<int>(e);
+  const long long rows = static_cast<long long>(a.B) * a.H * a.Nq;
+  hipLaunchKernelGGL((fa_decode_combine<T, D>), dim3(static_cast<unsigned>((rows + 3) / 4)),
+                     dim3(256), 0, stream, a);
+  return static_cast<int>(hipGetLastError());
+}
+
+}  // namespace m16
+}  // namespace fa

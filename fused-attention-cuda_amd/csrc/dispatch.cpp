@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -342,10 +343,111 @@ int forward_impl(int impl, int dtype, const void* q, const void* k, const void* 
 }  // namespace
 }  // namespace fa
 
+namespace fa {
+namespace {
+constexpr int kDecodeTile = 128;  // keys per tile of the decode split kernel
+
+// Why a decode call is invalid (nullptr when it is valid): hipErrorInvalidValue cases only.
+const char* decode_invalid(int dtype, const void* q, const void* k, const void* v, const void* o,
+                           const float* lse, const fa_decode_params* p) {
+  if (p == nullptr) return "null params";
+  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || lse == nullptr) {
+    return "null tensor pointer";
+  }
+  if (dtype < FA_DTYPE_F32 || dtype > FA_DTYPE_BF16) return "unknown dtype";
+  if (p->B < 1 || p->H < 1 || p->Hkv < 1 || p->Nq < 1 || p->Nkv < 1) return "non-positive size";
+  if (p->H % p->Hkv != 0) return "H must be a multiple of Hkv";
+  if (!(p->scale > 0.f) || !std::isfinite(p->scale)) return "scale must be finite and > 0";
+  if (p->num_splits < 0) return "num_splits must be >= 0";
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) {
+    return "q/k/v/o must be 16-byte aligned";
+  }
+  return nullptr;
+}
+
+int decode_splits(const fa_decode_params& p) {
+  const int tiles = (p.Nkv + kDecodeTile - 1) / kDecodeTile;
+  if (p.num_splits > 0) return std::min(p.num_splits, tiles);
+  // One workgroup per CU of a 256-CU part (measured best on MI355X against 2 per CU: the split
+  // kernel keeps a 64 KiB tile in flight per workgroup, and more splits only add prologues and
+  // combine work), each split at least four tiles long.
+  const long long groups = static_cast<long long>(p.B) * p.Hkv;
+  const long long want = (256 + groups - 1) / groups;
+  const int cap = std::max(1, tiles / 4);
+  return static_cast<int>(std::max<long long>(1, std::min<long long>(want, cap)));
+}
+}  // namespace
+}  // namespace fa
+
 // =============================================================================================
 // C-ABI (include/fa/attention.h)
 // =============================================================================================
 extern "C" {
+
+int fa_decode_num_splits(const fa_decode_params* p) {
+  if (p == nullptr || p->Nkv < 1 || p->B < 1 || p->Hkv < 1 || p->num_splits < 0) return 0;
+  return fa::decode_splits(*p);
+}
+
+size_t fa_decode_workspace_bytes(int /*dtype*/, const fa_decode_params* p) {
+  const int S = fa_decode_num_splits(p);
+  if (S <= 1 || p->Hkv < 1 || p->H % p->Hkv != 0) return 0;
+  const size_t rows = static_cast<size_t>(p->B) * p->Hkv * S * (p->H / p->Hkv) * p->Nq;
+  const size_t o_bytes = (rows * p->D * sizeof(float) + 255) / 256 * 256;
+  return o_bytes + (rows * sizeof(float) + 255) / 256 * 256;
+}
+
+int fa_decode(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+              void* workspace, const fa_decode_params* p, hipStream_t stream) {
+  if (const char* why = fa::decode_invalid(dtype, q, k, v, o, lse, p)) {
+    if (fa::verbose()) std::fprintf(stderr, "fa_decode: invalid params: %s\n", why);
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  int arch = 0;
+  if (const int e = fa_current_arch(&arch); e != 0) return e;
+  const int G = p->H / p->Hkv;
+  const fa::DecodeFn fn = arch != 950 ? nullptr
+                          : dtype == FA_DTYPE_F16 ? fa::decode_f16(p->D)
+                          : dtype == FA_DTYPE_BF16 ? fa::decode_bf16(p->D)
+                                                   : nullptr;
+  if (fn == nullptr || static_cast<long long>(G) * p->Nq > 32) {
+    if (fa::verbose()) {
+      std::fprintf(stderr, "fa_decode: not supported: dtype %s, D %d, (H/Hkv)*Nq %lld, gfx%d\n",
+                   fa_dtype_name(dtype), p->D, static_cast<long long>(G) * p->Nq, arch);
+    }
+    return static_cast<int>(hipErrorNotSupported);
+  }
+  fa::DecArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  a.B = p->B;
+  a.H = p->H;
+  a.Hkv = p->Hkv;
+  a.G = G;
+  a.Nq = p->Nq;
+  a.Nkv = p->Nkv;
+  a.R = G * p->Nq;
+  a.S = fa::decode_splits(*p);
+  const int tiles = (p->Nkv + fa::kDecodeTile - 1) / fa::kDecodeTile;
+  a.chunk = (tiles + a.S - 1) / a.S * fa::kDecodeTile;
+  a.S = (p->Nkv + a.chunk - 1) / a.chunk;  // no empty trailing split
+  a.scale = p->scale;
+  a.c = p->scale * 1.4426950408889634f;
+  a.causal = p->causal ? 1 : 0;
+  if (a.S > 1) {
+    if (workspace == nullptr || !fa::aligned16(workspace)) {
+      if (fa::verbose()) std::fprintf(stderr, "fa_decode: workspace missing or misaligned\n");
+      return static_cast<int>(hipErrorInvalidValue);
+    }
+    const size_t rows = static_cast<size_t>(a.B) * a.Hkv * a.S * a.R;
+    a.o_part = static_cast<float*>(workspace);
+    a.lse_part = a.o_part + (rows * p->D * sizeof(float) + 255) / 256 * 256 / sizeof(float);
+  }
+  return fn(a, stream);
+}
 
 int fa_current_arch(int* arch) {
   if (arch == nullptr) return static_cast<int>(hipErrorInvalidValue);

@@ -245,6 +245,58 @@ std::tuple<at::Tensor, at::Tensor> forward_stage_cuda(const at::Tensor& q, const
   return run_stage(q, k, v, is_causal, scale, stage);
 }
 
+// decode: split-KV decode (fa_decode). q [B, H, Nq, D]; k, v [B, Hkv, Nkv, D]; returns
+// (o [B, H, Nq, D], lse [B, H, Nq] fp32). No counterpart in the reference's op (its stated next
+// step, ref:README.md:1357-1358). The workspace is a byte tensor from the caching allocator,
+// released in stream order like the reference's stage workspace
+// (ref:python/fused_attn/ext.cpp:143-157).
+std::tuple<at::Tensor, at::Tensor> decode_cuda(const at::Tensor& q, const at::Tensor& k,
+                                               const at::Tensor& v, bool is_causal, double scale,
+                                               int64_t num_splits) {
+  TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(),
+              "fused_attn: decode inputs must be CUDA (HIP) tensors");
+  TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4,
+              "fused_attn: decode expects q [B, H, Nq, D] and k, v [B, Hkv, Nkv, D]");
+  TORCH_CHECK(q.scalar_type() == k.scalar_type() && q.scalar_type() == v.scalar_type(),
+              "fused_attn: q, k, v must share one dtype");
+  TORCH_CHECK(q.is_contiguous() && k.is_contiguous() && v.is_contiguous(),
+              "fused_attn: decode needs contiguous q, k, v");
+  TORCH_CHECK(k.sizes() == v.sizes(), "fused_attn: k and v must have the same shape");
+  TORCH_CHECK(q.size(0) == k.size(0) && q.size(3) == k.size(3),
+              "fused_attn: q and k must share B and D");
+  TORCH_CHECK(k.size(1) > 0 && q.size(1) % k.size(1) == 0,
+              "fused_attn: H must be a multiple of Hkv");
+  TORCH_CHECK(scale > 0.0, "fused_attn: scale must be > 0");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  fa_decode_params p{};
+  p.B = checked_int(q.size(0), "B");
+  p.H = checked_int(q.size(1), "H");
+  p.Hkv = checked_int(k.size(1), "Hkv");
+  p.Nq = checked_int(q.size(2), "Nq");
+  p.Nkv = checked_int(k.size(2), "Nkv");
+  p.D = checked_int(q.size(3), "D");
+  p.scale = static_cast<float>(scale);
+  p.causal = is_causal;
+  p.num_splits = checked_int(num_splits, "num_splits");
+  const int dtype = to_fa_dtype(q.scalar_type());
+  at::Tensor o = at::empty_like(q);
+  at::Tensor lse = at::empty({p.B, p.H, p.Nq}, q.options().dtype(at::kFloat));
+  const size_t ws_bytes = fa_decode_workspace_bytes(dtype, &p);
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+  const hipStream_t stream =
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.device().index()).stream();
+  const int err = fa_decode(dtype, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                            lse.data_ptr<float>(), ws_bytes > 0 ? ws.data_ptr() : nullptr, &p,
+                            stream);
+  TORCH_CHECK(err != static_cast<int>(hipErrorNotSupported),
+              "fused_attn: decode is not implemented for ", fa_dtype_name(dtype), " D=", p.D,
+              " with (H/Hkv)*Nq=", static_cast<int64_t>(p.H / p.Hkv) * p.Nq,
+              " (supported: fp16/bf16, D 64 or 128, (H/Hkv)*Nq <= 32, gfx950)");
+  TORCH_CHECK(err == 0, "fused_attn: decode failed: ", fa_error_string(err));
+  return {o, lse};
+}
+
 // TEST-ONLY: forces BR / BC (0 = default) for the tile-invariance tests; process-global.
 void set_debug_overrides_op(int64_t block_m, int64_t block_n) {
   fa_set_debug_overrides(checked_int(block_m, "block_m"), checked_int(block_n, "block_n"));
@@ -271,6 +323,10 @@ TORCH_LIBRARY(fused_attn, m) {
       " -> (Tensor, Tensor)");
   // Extension beyond the reference's frozen schemas: strided q/k/v views.
   m.def("forward_strided(Tensor q, Tensor k, Tensor v, bool is_causal, float scale) -> Tensor");
+  // Extension beyond the reference's frozen schemas: split-KV decode (Nq != Nkv).
+  m.def(
+      "decode(Tensor q, Tensor k, Tensor v, bool is_causal, float scale, int num_splits)"
+      " -> (Tensor, Tensor)");
   // Scalar-only ops have no dispatch key: their kernels are catch-alls.
   m.def("set_debug_overrides(int block_m, int block_n) -> ()", &set_debug_overrides_op);
   m.def("impl_supports(int stage, str dtype, int D) -> bool", &impl_supports_op);
@@ -281,6 +337,7 @@ TORCH_LIBRARY_IMPL(fused_attn, CUDA, m) {
   m.impl("forward", &forward_cuda);
   m.impl("forward_stage", &forward_stage_cuda);
   m.impl("forward_strided", &forward_strided_cuda);
+  m.impl("decode", &decode_cuda);
 }
 
 // Importing the .so runs the TORCH_LIBRARY static initialisers; the module exports nothing.

@@ -44,6 +44,34 @@ struct KArgs {
   int qsn, ksn, vsn, osn;
 };
 
+// Arguments of the split-KV decode kernels (attn_decode.h). q, o: [B, H, Nq, D]; k, v:
+// [B, Hkv, Nkv, D], all dense; lse [B, H, Nq]. o_part [B, Hkv, S, R, D] and lse_part
+// [B, Hkv, S, R] (fp32) live in the caller's workspace when S > 1.
+struct DecArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  float* o_part;
+  float* lse_part;
+  int B;
+  int H;
+  int Hkv;
+  int G;      // H / Hkv
+  int Nq;
+  int Nkv;
+  int R;      // G * Nq query rows per kv head, <= 32
+  int S;      // splits of the key range
+  int chunk;  // keys per split, a multiple of the 128-key tile
+  float scale;
+  float c;    // scale * log2(e)
+  int causal; // bottom-right: token i sees keys j <= Nkv - Nq + i
+};
+using DecodeFn = int (*)(const DecArgs& a, hipStream_t stream);
+DecodeFn decode_f16(int D);   // attn_f16.hip; nullptr for an unsupported D
+DecodeFn decode_bf16(int D);  // attn_bf16.hip
+
 // One instantiated (D, BR, BC) kernel of a stage, and the table of them per (stage, dtype).
 using LaunchFn = int (*)(const KArgs& a, hipStream_t stream);
 struct Variant {

@@ -18,8 +18,10 @@ Ops (schemas as in the reference, ref:python/fused_attn/ext.cpp:220-230)::
     torch.ops.fused_attn.forward(q, k, v, is_causal, scale) -> Tensor
     torch.ops.fused_attn.forward_stage(q, k, v, is_causal, scale, stage) -> (Tensor, Tensor)
 
-plus one extension: ``torch.ops.fused_attn.forward_strided(q, k, v, is_causal, scale) -> Tensor``
-over strided views (no counterpart in the reference).
+plus two extensions with no counterpart in the reference:
+``torch.ops.fused_attn.forward_strided(q, k, v, is_causal, scale) -> Tensor`` over strided views,
+and ``torch.ops.fused_attn.decode(q, k, v, is_causal, scale, num_splits) -> (Tensor, Tensor)``,
+split-KV decode of Nq new tokens against Nkv cached keys (the reference's stated next step).
 """
 
 from __future__ import annotations
@@ -33,6 +35,7 @@ from . import ops
 
 __all__ = [
     "__version__",
+    "decode",
     "forward",
     "forward_stage",
     "forward_strided",
@@ -100,6 +103,18 @@ def forward_strided(q: Tensor, k: Tensor, v: Tensor, is_causal: bool = False,
     reference op surface, which only takes contiguous tensors."""
     _require_ext()
     return torch.ops.fused_attn.forward_strided(q, k, v, bool(is_causal), _resolve_scale(q, scale))
+
+
+def decode(q: Tensor, k: Tensor, v: Tensor, is_causal: bool = False, scale: float | None = None,
+           num_splits: int = 0) -> tuple[Tensor, Tensor]:
+    """Split-KV decode: q [B, H, Nq, D] (the Nq newest tokens) against the cache k, v
+    [B, Hkv, Nkv, D] -> (o [B, H, Nq, D], lse [B, H, Nq]). With ``is_causal`` token i sees keys
+    j <= Nkv - Nq + i (bottom-right alignment). ``num_splits`` = 0 lets the library choose how
+    many pieces of the key range run in parallel; the pieces are combined with LSE weights.
+    fp16/bf16, D 64 or 128, (H / Hkv) * Nq <= 32."""
+    _require_ext()
+    return torch.ops.fused_attn.decode(q, k, v, bool(is_causal), _resolve_scale(q, scale),
+                                       int(num_splits))
 
 
 def impl_supports(stage: int, dtype: torch.dtype, head_dim: int) -> bool:

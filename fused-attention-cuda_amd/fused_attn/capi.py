@@ -28,9 +28,10 @@ DTYPE_CODES = {torch.float32: FA_DTYPE_F32, torch.float16: FA_DTYPE_F16,
                torch.bfloat16: FA_DTYPE_BF16}
 
 # Every function include/fa/attention.h declares, in declaration order.
-EXPORTS = ("fa_forward", "fa_forward_strided", "fa_workspace_bytes", "fa_impl_supports", "fa_set_debug_overrides",
-           "fa_get_debug_overrides", "fa_impl_name", "fa_dtype_name", "fa_dtype_size",
-           "fa_current_arch", "fa_error_string")
+EXPORTS = ("fa_forward", "fa_forward_strided", "fa_workspace_bytes", "fa_impl_supports",
+           "fa_set_debug_overrides", "fa_get_debug_overrides", "fa_impl_name", "fa_dtype_name",
+           "fa_dtype_size", "fa_current_arch", "fa_error_string", "fa_decode_num_splits",
+           "fa_decode_workspace_bytes", "fa_decode")
 
 
 class FaParams(ctypes.Structure):
@@ -45,6 +46,15 @@ class FaStrides(ctypes.Structure):
     """``fa_strides`` (include/fa/attention.h): per batch, per head, per row, in elements."""
 
     _fields_ = [("b", ctypes.c_longlong), ("h", ctypes.c_longlong), ("n", ctypes.c_longlong)]
+
+
+class FaDecodeParams(ctypes.Structure):
+    """``fa_decode_params`` (include/fa/attention.h)."""
+
+    _fields_ = [("B", ctypes.c_int), ("H", ctypes.c_int), ("Hkv", ctypes.c_int),
+                ("Nq", ctypes.c_int), ("Nkv", ctypes.c_int), ("D", ctypes.c_int),
+                ("scale", ctypes.c_float), ("causal", ctypes.c_bool),
+                ("num_splits", ctypes.c_int)]
 
 
 _lib: ctypes.CDLL | None = None
@@ -82,6 +92,13 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     lib.fa_dtype_size.restype = ctypes.c_size_t
     lib.fa_current_arch.argtypes = [ctypes.POINTER(ci)]
     lib.fa_current_arch.restype = ci
+    dp = ctypes.POINTER(FaDecodeParams)
+    lib.fa_decode_num_splits.argtypes = [dp]
+    lib.fa_decode_num_splits.restype = ci
+    lib.fa_decode_workspace_bytes.argtypes = [ci, dp]
+    lib.fa_decode_workspace_bytes.restype = ctypes.c_size_t
+    lib.fa_decode.argtypes = [ci, vp, vp, vp, vp, vp, vp, dp, vp]
+    lib.fa_decode.restype = ci
     lib.fa_error_string.argtypes = [ci]
     lib.fa_error_string.restype = ctypes.c_char_p
     if path is None:
@@ -139,3 +156,26 @@ def forward_strided(impl: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
                                      k.data_ptr(), ctypes.byref(ks), v.data_ptr(),
                                      ctypes.byref(vs), o.data_ptr(), ctypes.byref(os_),
                                      lse.data_ptr(), None, ctypes.byref(p), s.cuda_stream)
+
+
+def decode_params(q: torch.Tensor, k: torch.Tensor, is_causal: bool, scale: float,
+                  num_splits: int = 0) -> FaDecodeParams:
+    """``fa_decode_params`` for q [B, H, Nq, D] and k [B, Hkv, Nkv, D]."""
+    b, h, nq, d = q.shape
+    return FaDecodeParams(b, h, k.shape[1], nq, k.shape[2], d, scale, is_causal, num_splits)
+
+
+def decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, lse: torch.Tensor,
+           is_causal: bool, scale: float, num_splits: int = 0, workspace: torch.Tensor | None = None,
+           stream: torch.cuda.Stream | None = None) -> int:
+    """``fa_decode`` on torch device tensors; allocates the workspace the library asks for unless
+    one is given. Returns the hipError_t value."""
+    lib = load()
+    p = decode_params(q, k, is_causal, scale, num_splits)
+    if workspace is None:
+        nbytes = lib.fa_decode_workspace_bytes(DTYPE_CODES.get(q.dtype, -1), ctypes.byref(p))
+        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    s = stream if stream is not None else torch.cuda.current_stream(q.device)
+    return lib.fa_decode(DTYPE_CODES.get(q.dtype, -1), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                         o.data_ptr(), lse.data_ptr(), workspace.data_ptr(), ctypes.byref(p),
+                         s.cuda_stream)

@@ -76,6 +76,16 @@ def _fake_forward_strided(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, scal
     return empty_in_layout_of(q)
 
 
+def _fake_decode(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, scale: float,
+                 num_splits: int) -> tuple[Tensor, Tensor]:
+    torch._check(q.dim() == 4 and k.dim() == 4 and v.dim() == 4,
+                 lambda: "decode expects q [B, H, Nq, D] and k, v [B, Hkv, Nkv, D]")
+    b, h, nq, d = q.shape
+    torch._check(q.dtype == k.dtype and q.dtype == v.dtype, lambda: "q/k/v must share one dtype")
+    torch._check(k.shape[1] > 0 and h % k.shape[1] == 0, lambda: "H must be a multiple of Hkv")
+    return torch.empty_like(q), q.new_empty((b, h, nq), dtype=torch.float32)
+
+
 def register_fakes() -> None:
     """Register the fake kernels (idempotent; requires ``fused_attn._C`` to be loaded)."""
     global _registered
@@ -84,6 +94,7 @@ def register_fakes() -> None:
     torch.library.register_fake("fused_attn::forward", _fake_forward)
     torch.library.register_fake("fused_attn::forward_stage", _fake_forward_stage)
     torch.library.register_fake("fused_attn::forward_strided", _fake_forward_strided)
+    torch.library.register_fake("fused_attn::decode", _fake_decode)
     _registered = True
 
 

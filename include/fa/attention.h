@@ -120,6 +120,45 @@ FA_API int fa_current_arch(int* arch);
 /* Human-readable text for a status returned by this library (hipGetErrorString). */
 FA_API const char* fa_error_string(int status);
 
+/* ---- split-KV decode (flash-decoding) ------------------------------------------------------
+ * No counterpart in the reference's API: it is the reference's own next step (ref:README.md:
+ * 1357-1358, "partial O + LSE per split, LSE-weighted combine"), built on the LSE output it emits
+ * (ref:include/fa/softmax_math.cuh:65-68). Nq new query tokens per sequence attend to Nkv cached
+ * keys. Layouts (dense, D fastest): q, o [B, H, Nq, D]; k, v [B, Hkv, Nkv, D]; lse [B, H, Nq] fp32
+ * natural log, +inf for a row that sees no key. Query head h reads kv head h / (H / Hkv).
+ * With `causal` the new tokens are the last Nq positions (bottom-right alignment): token i sees
+ * keys j <= Nkv - Nq + i; without it every token sees all Nkv keys.
+ * Contract: dtype fp16 or bf16, D in {64, 128}, Nq >= 1, Nkv >= 1 (any length), H % Hkv == 0,
+ * (H / Hkv) * Nq <= 32 (the query rows of one kv head fill one 32-row tile), finite scale > 0,
+ * 16-byte aligned q/k/v/o. */
+typedef struct fa_decode_params {
+  int B;          /* batch */
+  int H;          /* query heads */
+  int Hkv;        /* key/value heads, H % Hkv == 0 */
+  int Nq;         /* new query tokens per sequence */
+  int Nkv;        /* cached keys per sequence */
+  int D;          /* head dimension, 64 or 128 */
+  float scale;    /* softmax scale applied to q.k */
+  bool causal;    /* bottom-right aligned causal mask */
+  int num_splits; /* splits of the key range; 0 = chosen by the library */
+} fa_decode_params;
+
+/* Splits fa_decode uses for these parameters (num_splits if > 0, capped so that every split
+ * holds at least one 128-key tile; otherwise enough to fill the GPU). 0 for invalid params. */
+FA_API int fa_decode_num_splits(const fa_decode_params* p);
+
+/* Bytes of workspace fa_decode needs: fp32 partial O and LSE of every split,
+ * B*Hkv*S*R*(D+1)*4 rounded up, with R = (H/Hkv)*Nq and S = fa_decode_num_splits(p); 0 when
+ * S == 1 (the single split writes o and lse directly). */
+FA_API size_t fa_decode_workspace_bytes(int dtype, const fa_decode_params* p);
+
+/* Runs the decode: one split kernel (all splits in parallel) and, when S > 1, one combine
+ * kernel, asynchronously on `stream`. Returns a hipError_t value: hipErrorInvalidValue for
+ * invalid parameters, misaligned pointers or a missing workspace; hipErrorNotSupported for a
+ * dtype, D, row count or device this build does not cover. Allocates nothing. */
+FA_API int fa_decode(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+                     void* workspace, const fa_decode_params* p, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

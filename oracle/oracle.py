@@ -47,6 +47,9 @@ __all__ = [
     "COracle",
     "RatioResult",
     "RefOracle",
+    "combine_splits",
+    "decode_keep_mask",
+    "decode_reference",
     "default_scale",
     "error_ratio",
     "keep_mask",
@@ -127,6 +130,44 @@ def math_reference(q, k, v, is_causal: bool = False, scale: float | None = None,
         lse = np.where(l_row == 0, np.inf, m_safe + np.log(np.where(l_row == 0, 1.0, l_row)))
     o = np.matmul(p, v64) * inv_l
     return o, lse[..., 0]
+
+
+def decode_keep_mask(n_q: int, n_kv: int, is_causal: bool) -> np.ndarray | None:
+    """Keep mask of split-KV decode: the n_q new tokens are the last positions of the sequence,
+    so with ``is_causal`` token i sees keys j <= n_kv - n_q + i (bottom-right alignment, what a KV
+    cache means); without it every token sees every key. For n_q == n_kv this is the top-left
+    mask of :func:`keep_mask`. There is no reference implementation (decode is the reference's
+    stated next step, ref:README.md:1357-1358); the tests pin this against torch SDPA MATH with
+    torch's own ``tril`` mask and brute-force loops."""
+    if not is_causal:
+        return None
+    return np.tril(np.ones((n_q, n_kv), dtype=bool), k=n_kv - n_q)
+
+
+def decode_reference(q, k, v, is_causal: bool = False, scale: float | None = None):
+    """fp64 split-KV decode answer: q [B, H, Nq, D] against k, v [B, Hkv, Nkv, D] with the
+    bottom-right mask -> ``(o, lse)``; rows with no visible key give o = 0, lse = +inf."""
+    nq, nkv = q.shape[2], k.shape[2]
+    return math_reference(q, k, v, is_causal=False, scale=scale,
+                          attn_mask=decode_keep_mask(nq, nkv, is_causal))
+
+
+def combine_splits(o_parts, lse_parts):
+    """LSE-weighted combine of per-split partials (ref:docs/RESEARCH.md:151-156):
+    O = sum_s e^(L_s - L*) O_s / sum_s e^(L_s - L*), L = L* + ln sum_s e^(L_s - L*), L* = max_s L_s.
+    ``o_parts`` [S, ..., D], ``lse_parts`` [S, ...]; an empty split carries L_s = -inf and weight
+    0; a row whose splits are all empty gives O = 0 and L = +inf."""
+    o_parts = np.asarray(o_parts, dtype=np.float64)
+    lse_parts = np.asarray(lse_parts, dtype=np.float64)
+    lmax = lse_parts.max(axis=0)
+    lmax_safe = np.where(np.isneginf(lmax), 0.0, lmax)
+    w = np.exp(lse_parts - lmax_safe)
+    wsum = w.sum(axis=0)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        o = np.where(wsum[..., None] > 0, (w[..., None] * o_parts).sum(axis=0) / wsum[..., None],
+                     0.0)
+        lse = np.where(wsum > 0, lmax_safe + np.log(np.where(wsum > 0, wsum, 1.0)), np.inf)
+    return o, lse
 
 
 def math_reference_rows(q, k, v, b: int, h: int, rows, is_causal: bool = False,
