@@ -244,6 +244,28 @@ struct Fa16 {
   // Waits until this wave's LDS-DMA loads have landed (vmcnt(0); expcnt and lgkmcnt untouched).
   __device__ static void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+  // One 1 KiB LDS-DMA instruction from inline assembly. The compiler does not see it as a load
+  // that may write LDS, so it adds no vmcnt wait of its own before later LDS reads; the caller
+  // waits for it explicitly (wait_dma) before the barrier that publishes the tile.
+  __device__ static void dma_asm(const void* src, const void* lds) {
+    uint32_t m0;
+    asm volatile("s_mov_b32 %0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 : "={m0}"(m0)
+                 : "v"(src), "s"(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)))
+                 : "memory");
+  }
+  // dma_tile through dma_asm (rows past the last key read row N-1, as in dma_tile).
+  template <bool IS_V>
+  __device__ static void dma_tile_asm(T* buf, const T* gbase, const Dma& d, int k0, int N, int sn,
+                                      int wave) {
+    const T* tile = gbase + static_cast<ptrdiff_t>(k0) * sn;
+#pragma unroll
+    for (int i = 0; i < kDmaPerWave; ++i) {
+      const int last = min(d.row[i], N - 1 - k0);
+      dma_asm(tile + d.off[i] + (last - d.row[i]) * sn, buf + 512 * (wave + i * kWaves));
+    }
+  }
+
   struct WaveState {
     u32x4 q[D / 16];  // B operand of S^T: row n = l%32, head-dim 16*st + 8*(l/32) .. +7
     f32x16 o[kDB];    // O^T accumulator: head-dim rows, query-row columns
@@ -604,14 +626,20 @@ struct Fa16 {
         const T* kn = kwave((t + 1) & 1);
         const T* vc = vwave(t & 1);
         if constexpr (kFull) {
-          // Steady steps have K(t+2) and V(t+1) inside the tensor (see n_steady).
+          // The tiles loaded are clamped to the last one: past the end of the key range (the last
+          // two steps when every tile is full) the copies land in buffers that are not read again
+          // (the last step's S(t+1) is computed from a stale K buffer and discarded), which keeps
+          // the tail on this branch-free body.
+          const int tk = min(t + 2, n_tiles - 1), tv = min(t + 1, n_tiles - 1);
           step_full(ws, s_cur, s_nxt, P, kn, vc, kl, vl, c, lane, [&] {
-            dma_tile_full<false>(kbuf0 + (t & 1) * kKElems, kg, dk, (t + 2) * BC, ksn, wave);
-            dma_tile_full<true>(vbuf0 + ((t + 1) & 1) * kVElems, vg, dv, (t + 1) * BC, vsn, wave);
+            dma_tile_full<false>(kbuf0 + (t & 1) * kKElems, kg, dk, tk * BC, ksn, wave);
+            dma_tile_full<true>(vbuf0 + ((t + 1) & 1) * kVElems, vg, dv, tv * BC, vsn, wave);
           });
         } else {
-          if (t + 2 < n_tiles) dma_tile<false>(kbuf0 + (t & 1) * kKElems, kg, dk, (t + 2) * BC, N, ksn, wave);
-          if (t + 1 < n_tiles) dma_tile<true>(vbuf0 + ((t + 1) & 1) * kVElems, vg, dv, (t + 1) * BC, N, vsn, wave);
+          // LDS-DMA from inline assembly: the compiler would otherwise make the LDS reads below
+          // wait for these loads, which target buffers this iteration does not read.
+          if (t + 2 < n_tiles) dma_tile_asm<false>(kbuf0 + (t & 1) * kKElems, kg, dk, (t + 2) * BC, N, ksn, wave);
+          if (t + 1 < n_tiles) dma_tile_asm<true>(vbuf0 + ((t + 1) & 1) * kVElems, vg, dv, (t + 1) * BC, N, vsn, wave);
           const int nv = nvalid_of(t);
           const int dg = diag_of(t, nv);
           const int nv_nxt = (t + 1 < n_tiles) ? nvalid_of(t + 1) : 0;
@@ -631,10 +659,13 @@ struct Fa16 {
       using P0 = std::integral_constant<int, 0>;
       using P1 = std::integral_constant<int, 1>;
       // Tiles [0, n_full) are full for every wave and carry no diagonal (workgroup-uniform): key
-      // tile t is complete below the workgroup's first row (causal) or below N.
+      // tile t is complete below the workgroup's first row (causal) or below N. When every tile is
+      // full (non-causal, N a multiple of BC) all of them take the steady step; otherwise steady
+      // step t also needs tile t+1 full and K(t+2) a whole tile inside the tensor
+      // (t + 3 <= N / BC), so that its loads need no clamp.
       const int n_full = (a.causal ? i0 : N) / BC;
-      // Steady step t also needs K(t+2) to be a whole tile inside the tensor: t + 3 <= N / BC.
-      const int n_steady = max(0, min(min(n_tiles, n_full) - 1, N / BC - 2));
+      const int n_steady = n_full >= n_tiles ? n_tiles
+                                             : max(0, min(min(n_tiles, n_full) - 1, N / BC - 2));
       // Unrolled by two so the S(t) / S(t+1) register sets swap roles without copies; the steady
       // loop and the tail loop get independent register assignments.
       int t = 0;
