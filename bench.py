@@ -219,6 +219,27 @@ def bench_workload(torch, capi, name, stage, steps, warmup, seed=0, gate_it=True
     return res, sets, stream, causal, scale
 
 
+def sdpa_ms(torch, sets, causal, scale, stream, steps, warmup):
+    """torch.nn.functional.scaled_dot_product_attention (the backend torch selects on ROCm) on the
+    same rotating inputs, timed like the fused op: back to back, one event pair around the loop on
+    the launch stream. This is the reference's own denominator (it reports each stage as a
+    fraction of the vendor SDPA, ref:README.md:97-100)."""
+    import torch.nn.functional as F
+
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            q, k, v = sets[i % len(sets)][:3]
+            F.scaled_dot_product_attention(q, k, v, is_causal=causal, scale=scale)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            q, k, v = sets[i % len(sets)][:3]
+            F.scaled_dot_product_attention(q, k, v, is_causal=causal, scale=scale)
+        e1.record(stream)
+    stream.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
 def decode_line(torch):
     """Split-KV decode (fa_decode): one new token per sequence against a bf16 KV cache,
     B8 H32 Hkv8 Nkv8192 D128 (a GQA 4:1 model at 8K context). The kernel is HBM-bound: its
@@ -316,6 +337,9 @@ def main(argv=None) -> int:
     b, h, n, d, dt = head["B"], head["H"], head["N"], head["D"], head["dtype"]
     achieved = head["tflops"]
     esize = 2 if dt in ("fp16", "bf16") else 4
+    vendor = None
+    if not a.only and head["dtype"] == "fp16":
+        vendor = sdpa_ms(torch, sets, causal, scale, stream, a.steps, a.warmup)
     line = {
         "metric": METRIC,
         "value": round(achieved, 3),
@@ -343,6 +367,9 @@ def main(argv=None) -> int:
         "pct_of_peak": round(head["pct_peak"], 3),
         "gate": {"max_err_o": head["gate_max_err_o"], "max_err_lse": head["gate_max_err_lse"]},
     }
+    if vendor is not None:
+        line["vendor_sdpa"] = {"ms": round(vendor, 6), "fused_speedup": round(vendor / head["ms"], 3),
+                               "what": "torch scaled_dot_product_attention, same inputs, fp16"}
     if not a.only:
         line["protocol"] = protocol_timing(torch, capi, sets, causal, scale, a.stage, stream)
         q, k, v, o, lse = sets[0]
@@ -354,8 +381,13 @@ def main(argv=None) -> int:
                 continue
             # Each secondary config gets its own long warm-up: it follows a different workload
             # (and the CPU baseline's idle GPU), and the clock settles within tens of launches.
-            res, s2, _, _, _ = bench_workload(torch, capi, name, 5, max(50, a.steps // 2),
-                                              max(50, a.warmup))
+            res, s2, st2, c2, sc2 = bench_workload(torch, capi, name, 5, max(50, a.steps // 2),
+                                                   max(50, a.warmup))
+            # Vendor SDPA beside the fp16 configs only: its bf16 fallback path goes through
+            # batched products on transposed views, which have faulted on these boxes.
+            if res["dtype"] == "fp16":
+                res["vendor_sdpa_ms"] = sdpa_ms(torch, s2, c2, sc2, st2, max(50, a.steps // 2),
+                                                max(50, a.warmup))
             del s2
             others[name] = {kk: (round(vv, 6) if isinstance(vv, float) else vv)
                             for kk, vv in res.items()}
