@@ -237,6 +237,9 @@ __global__ __launch_bounds__(256) void fa_decode_split(DecArgs a) {
 // head-dim elements [D/64 * l, D/64 * (l + 1)). lse = L* + ln(sum_s e^(L_s - L*)); a row whose
 // splits are all empty gets O = 0 and lse = +inf (the non-split convention,
 // ref:include/fa/softmax_math.cuh:62-68).
+// The kernel is a couple of memory round trips per row, so it keeps them few: the splits' LSE are
+// read by one lane each (64 splits per load), reduced across the wave, and the partial rows are
+// read eight splits per batch of independent loads.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void fa_decode_combine(DecArgs a) {
   constexpr int kPer = D / 64;
@@ -251,20 +254,50 @@ __global__ __launch_bounds__(256) void fa_decode_combine(DecArgs a) {
   const int hkv = h / a.G;
   const int r = (h - hkv * a.G) * a.Nq + i;
   const size_t base = static_cast<size_t>(b * a.Hkv + hkv) * a.S * a.R + r;  // split 0
+  const int S = a.S;
   float mx = -__builtin_inff();
-  for (int s = 0; s < a.S; ++s) mx = fmaxf(mx, a.lse_part[base + static_cast<size_t>(s) * a.R]);
+  for (int s0 = 0; s0 < S; s0 += 64) {
+    const int sl = s0 + lane;
+    mx = fmaxf(mx, sl < S ? a.lse_part[base + static_cast<size_t>(sl) * a.R] : -__builtin_inff());
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
   float acc[kPer];
 #pragma unroll
   for (int e = 0; e < kPer; ++e) acc[e] = 0.f;
   float wsum = 0.f;
   if (mx != -__builtin_inff()) {
-    for (int s = 0; s < a.S; ++s) {
-      const size_t pr = base + static_cast<size_t>(s) * a.R;
-      const float w = __expf(a.lse_part[pr] - mx);
-      wsum += w;
-      const float* src = a.o_part + pr * D + kPer * lane;
+    for (int s0 = 0; s0 < S; s0 += 64) {
+      const int sl = s0 + lane;
+      // This lane's split weight e^(L_s - L*); 0 past S (and for empty splits, L_s = -inf).
+      const float wl = sl < S ? __expf(a.lse_part[base + static_cast<size_t>(sl) * a.R] - mx) : 0.f;
+      float ws = wl;
 #pragma unroll
-      for (int e = 0; e < kPer; ++e) acc[e] += w * src[e];
+      for (int off = 32; off >= 1; off >>= 1) ws += __shfl_xor(ws, off);
+      wsum += ws;
+      const int n = min(64, S - s0);
+      const float* src0 = a.o_part + (base + static_cast<size_t>(s0) * a.R) * D + kPer * lane;
+      const size_t step = static_cast<size_t>(a.R) * D;
+      int j = 0;
+      for (; j + 8 <= n; j += 8) {
+        float v[8][kPer];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+#pragma unroll
+          for (int e = 0; e < kPer; ++e) v[u][e] = src0[(j + u) * step + e];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const float w = __shfl(wl, j + u);
+#pragma unroll
+          for (int e = 0; e < kPer; ++e) acc[e] += w * v[u][e];
+        }
+      }
+      for (; j < n; ++j) {
+        const float w = __shfl(wl, j);
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) acc[e] += w * src0[j * step + e];
+      }
     }
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;

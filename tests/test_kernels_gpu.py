@@ -74,6 +74,21 @@ def test_matches_fp64_reference(stage, dtype, causal, gpu_shape, make_qkv):
     check_against_reference(o, q, k, v, causal, dtype, lse=lse)
 
 
+# Stage 5 runs every key tile through its steady step when all tiles are full (non-causal, N a
+# multiple of the default BC: 128 at D = 64, 64 at D = 128); the last two steps then load clamped
+# tiles into buffers nobody reads again. These lengths give 1 to 5 full tiles (odd and even
+# counts, so the unrolled-by-two loop ends on either parity) plus one ragged length.
+@pytest.mark.parametrize("n,d", [(128, 64), (384, 64), (640, 64), (64, 128), (192, 128),
+                                 (320, 128), (160, 128)],
+                         ids=lambda x: str(x))
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=_pair_id)
+def test_stage5_full_tile_counts(n, d, dtype, make_qkv):
+    require(5, dtype, d)
+    q, k, v = make_qkv(1, 3, n, d, dtype=dtype, device="cuda")
+    o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=False)
+    check_against_reference(o, q, k, v, False, dtype, lse=lse)
+
+
 @pytest.mark.parametrize("stage", [1, 2])
 def test_unbuilt_stages_raise_not_implemented(stage, make_qkv):
     if not fused_attn.is_available():
