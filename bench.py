@@ -5,7 +5,10 @@ Headline workload: C64 = B2 H8 N2048 D64, fp16 in / fp32 a
 non-causal, through the stage-5 kernel (``fa_s5_tuned``, what ``torch.ops.fused_attn.forward``
 dispatches to for fp16). A *step* is one forward over one batch of synthetic inputs already
 resident in HBM. The kernel is launched through the C-ABI (``fa_forward`` of libfa_hip.so) on a
-dedicated HIP stream, and HIP events recorded on that same stream bracket the K timed steps.
+dedicated HIP stream. The K timed steps are those launches captured once into a HIP graph and
+replayed (the execution mode of a serving loop; every output of two checked replays is compared
+bitwise with eager launches first), bracketed by HIP events recorded on that same stream. The same
+K launches issued one by one from the host are reported beside it (``eager_launches``).
 
 Printed: ONE JSON line with the contract fields, plus
 * ``roofline``: MFMA-bound; achieved = 4*B*H*N^2*D FLOPs per launch / average launch duration;
@@ -15,7 +18,8 @@ Printed: ONE JSON line with the contract fields, plus
   kind "reference"; the C restatement, kind "port", when _ref is absent) timed on the host cores
   over the same workload, repeated for a bounded budget of CPU time;
 * ``configs``: the other BASELINE configurations measured the same way (C128, C128 causal, LONG,
-  GPT attention shape), each with ms and TFLOP/s;
+  GPT attention shape), each with ms and TFLOP/s (graph replay) and ``eager_ms``;
+* ``vendor_sdpa``: torch's ``scaled_dot_product_attention`` on the same inputs (fp16 configs);
 * ``protocol``: the reference's timing protocol (ref:docs/BENCHMARK_PROTOCOL.md rules 1-2) on the
   headline workload: 1 GiB flush before every launch, one event pair per launch, median/p10/p90.
 
@@ -102,7 +106,8 @@ def gate(torch, capi, q, k, v, o, lse, causal, scale, stage, stream):
 
 
 def time_steps(torch, capi, args_list, causal, scale, stage, stream, steps, warmup):
-    """Warmup, then K launches bracketed by events on the launch stream; average ms per launch.
+    """Warmup, then K launches bracketed by events on the launch stream; average ms per launch
+    (None when K is 0: warm-up only).
     args_list rotates over input sets (q, k, v, o, lse). The fa_forward arguments of each set are
     marshalled once, so the timed loop is one C call per launch and the host stays ahead of the
     GPU."""
@@ -125,6 +130,8 @@ def time_steps(torch, capi, args_list, causal, scale, stage, stream, steps, warm
     for i in range(warmup):
         launch(calls[i % len(calls)])
     stream.synchronize()
+    if steps == 0:
+        return None
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for i in range(steps):
@@ -132,6 +139,43 @@ def time_steps(torch, capi, args_list, causal, scale, stage, stream, steps, warm
     end.record(stream)
     end.synchronize()
     return start.elapsed_time(end) / steps
+
+
+def graph_timing(torch, capi, args_list, causal, scale, stage, stream, steps):
+    """The same ``steps`` launches captured once into a HIP graph (torch.cuda.CUDAGraph on the
+    launch stream) and replayed: the execution mode of a serving loop. Before timing, the graph is
+    replayed twice with the outputs cleared in between and every output compared bitwise with one
+    eager launch per input set (the kernel is deterministic). Returns ms per launch."""
+    with torch.cuda.stream(stream):  # one eager launch per set: the reference outputs
+        for q, k, v, o, lse in args_list:
+            capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream)
+    stream.synchronize()
+    eager = [(o.clone(), lse.clone()) for _, _, _, o, lse in args_list]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            q, k, v, o, lse = args_list[i % len(args_list)]
+            capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream)
+    for _ in range(2):
+        for _, _, _, o, lse in args_list:
+            o.zero_()
+            lse.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()
+        stream.synchronize()
+        for (o_ref, l_ref), (_, _, _, o, lse) in zip(eager, args_list):
+            if not (torch.equal(o, o_ref) and torch.equal(lse, l_ref)):
+                raise RuntimeError("graph replay differs from the eager launches")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        graph.replay()
+        e1.record(stream)
+    e1.synchronize()
+    del graph
+    return e0.elapsed_time(e1) / steps
 
 
 def protocol_timing(torch, capi, args_list, causal, scale, stage, stream, iters=100):
@@ -196,7 +240,11 @@ def cpu_baseline(q, k, v, causal, scale, gpu_o, budget_s: float):
             "ms_per_forward": wall / reps * 1e3}
 
 
-def bench_workload(torch, capi, name, stage, steps, warmup, seed=0, gate_it=True):
+def bench_workload(torch, capi, name, stage, steps, warmup, seed=0, gate_it=True, eager=True):
+    """Builds the workload's 4 rotating input sets on a fresh stream, gates the output against the
+    fp64 oracle, then times `steps` launches replayed from a HIP graph (``ms``) and, when `eager`,
+    the same launches issued one by one (``eager_ms``; otherwise only the warm-up runs, which
+    also produce the eager outputs the graph replays are checked against)."""
     b, h, n, d, dt, causal, std = WORKLOADS[name]
     dtype = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[dt]
     scale = 1.0 / math.sqrt(d)
@@ -210,12 +258,15 @@ def bench_workload(torch, capi, name, stage, steps, warmup, seed=0, gate_it=True
             sets.append((q, k, v, o, lse))
     stream.synchronize()
     err = gate(torch, capi, *sets[0], causal, scale, stage, stream) if gate_it else (None, None)
-    ms = time_steps(torch, capi, sets, causal, scale, stage, stream, steps, warmup)
+    eager_ms = time_steps(torch, capi, sets, causal, scale, stage, stream,
+                          steps if eager else 0, warmup)
+    ms = graph_timing(torch, capi, sets, causal, scale, stage, stream, steps)
     f = flops(b, h, n, d, causal)
     tf = f / (ms * 1e-3) / 1e12
     res = {"B": b, "H": h, "N": n, "D": d, "dtype": dt, "causal": causal, "stage": stage,
            "ms": ms, "tflops": tf, "pct_peak": 100.0 * tf / PEAK_TFLOPS[dt], "flops": f,
-           "gate_max_err_o": err[0], "gate_max_err_lse": err[1]}
+           "eager_ms": eager_ms if eager else None, "gate_max_err_o": err[0],
+           "gate_max_err_lse": err[1]}
     return res, sets, stream, causal, scale
 
 
@@ -332,8 +383,10 @@ def main(argv=None) -> int:
         print(json.dumps({"copy_probe_bytes": n, "launches": 5}))
         return 0
     capi.load()
+    # Under --only (the profiled command) the eager loop is skipped, so that the kernel trace's
+    # average duration is that of the timed graph replays.
     head, sets, stream, causal, scale = bench_workload(torch, capi, a.workload, a.stage, a.steps,
-                                                       a.warmup)
+                                                       a.warmup, eager=not a.only)
     b, h, n, d, dt = head["B"], head["H"], head["N"], head["D"], head["dtype"]
     achieved = head["tflops"]
     esize = 2 if dt in ("fp16", "bf16") else 4
@@ -367,9 +420,18 @@ def main(argv=None) -> int:
         "pct_of_peak": round(head["pct_peak"], 3),
         "gate": {"max_err_o": head["gate_max_err_o"], "max_err_lse": head["gate_max_err_lse"]},
     }
+    if head["eager_ms"] is not None:
+        etf = head["flops"] / (head["eager_ms"] * 1e-3) / 1e12
+        line["eager_launches"] = {"ms_per_step": round(head["eager_ms"], 6),
+                                  "tflops": round(etf, 3),
+                                  "pct_of_peak": round(100.0 * etf / PEAK_TFLOPS[dt], 3),
+                                  "what": "the same K launches issued one by one from the host "
+                                          "(ctypes -> fa_forward), one event pair around the loop"}
     if vendor is not None:
-        line["vendor_sdpa"] = {"ms": round(vendor, 6), "fused_speedup": round(vendor / head["ms"], 3),
-                               "what": "torch scaled_dot_product_attention, same inputs, fp16"}
+        line["vendor_sdpa"] = {"ms": round(vendor, 6),
+                               "fused_speedup_eager": round(vendor / head["eager_ms"], 3),
+                               "what": "torch scaled_dot_product_attention on the same inputs, "
+                                       "launched one by one (compare with eager_launches)"}
     if not a.only:
         line["protocol"] = protocol_timing(torch, capi, sets, causal, scale, a.stage, stream)
         q, k, v, o, lse = sets[0]
