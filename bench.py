@@ -17,8 +17,9 @@ Printed: ONE JSON line with the contract fields, plus
 * ``cpu_baseline``: the reference's own fp64 CPU oracle (oracle/_ref, ``fa::ref::attention_rows``,
   kind "reference"; the C restatement, kind "port", when _ref is absent) timed on the host cores
   over the same workload, repeated for a bounded budget of CPU time;
-* ``configs``: the other BASELINE configurations measured the same way (C128, C128 causal, LONG,
-  GPT attention shape), each with ms and TFLOP/s (graph replay) and ``eager_ms``;
+* ``configs``: the other BASELINE configurations measured the same way (C128, C128 causal, LONG
+  with its N sweep 512 / 1024 / 4096 / 8192, GPT attention shape), each with ms and TFLOP/s
+  (graph replay) and ``eager_ms``;
 * ``vendor_sdpa``: torch's ``scaled_dot_product_attention`` on the same inputs (fp16 configs);
 * ``protocol``: the reference's timing protocol (ref:docs/BENCHMARK_PROTOCOL.md rules 1-2) on the
   headline workload: 1 GiB flush before every launch, one event pair per launch, median/p10/p90.
@@ -51,6 +52,10 @@ WORKLOADS = {
     "C128_causal": (2, 8, 2048, 128, "fp16", True, 1.0),
     "LONG": (1, 16, 8192, 128, "bf16", True, 0.5),
     "GPT_attn": (8, 12, 1024, 64, "fp16", True, 1.0),
+    # The rest of BASELINE config 4's sweep (N in 512 / 1024 / 4096 beside LONG's 8192).
+    "LONG_N512": (1, 16, 512, 128, "bf16", True, 0.5),
+    "LONG_N1024": (1, 16, 1024, 128, "bf16", True, 0.5),
+    "LONG_N4096": (1, 16, 4096, 128, "bf16", True, 0.5),
 }
 
 

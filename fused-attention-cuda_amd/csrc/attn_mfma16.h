@@ -819,13 +819,15 @@ struct S5Rows {
   };
 };
 
-// BR 128 / BC 128 (4 row groups x 2 key splits of 64 keys, the D = 64 default) at D = 64 only.
+// At D = 64 only: BR 128 / BC 128 (4 row groups x 2 key splits of 64 keys, the D = 64 default)
+// and BR 32 / BC 128 (the same waves, one row group), the height small grids are launched with.
 template <typename T>
 VariantList s5_table() {
   static const Variant t[] = {
       S5Rows<T, 64>::rows[0],  S5Rows<T, 64>::rows[1],  S5Rows<T, 64>::rows[2],
       S5Rows<T, 64>::rows[3],  S5Rows<T, 64>::rows[4],  S5Rows<T, 64>::rows[5],
       S5Rows<T, 64>::rows[6],  S5Rows<T, 64>::rows[7],  variant<5, T, 64, 4, 2, 64>(),
+      variant<5, T, 64, 1, 2, 64>(),
       S5Rows<T, 128>::rows[0], S5Rows<T, 128>::rows[1], S5Rows<T, 128>::rows[2],
       S5Rows<T, 128>::rows[3], S5Rows<T, 128>::rows[4], S5Rows<T, 128>::rows[5],
       S5Rows<T, 128>::rows[6], S5Rows<T, 128>::rows[7]};

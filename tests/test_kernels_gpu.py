@@ -30,8 +30,8 @@ STAGE_DTYPE_PAIRS = [(s, dt) for s in (3, 4, 5) for dt in STAGE_DTYPES[s]]
 # Instantiated (BR, BC) tiles per stage (csrc/attn_mfma16.h and csrc/attn_kernel.h tables;
 # 0 = default). Stages 3 and 4 fix BR at 128 and ignore a forced BR, as the reference's S3/S4 do.
 STAGE_BC = {3: {32, 64}, 4: {32, 64, 128}}
-S5_TILES = {(32, 32), (32, 64), (64, 32), (64, 64), (64, 128), (128, 32), (128, 64), (128, 128),
-            (256, 64)}
+S5_TILES = {(32, 32), (32, 64), (32, 128), (64, 32), (64, 64), (64, 128), (128, 32), (128, 64),
+            (128, 128), (256, 64)}
 S5_DEFAULT = (128, 128)  # at D = 64, the head dim of the tile tests
 
 _ids = {torch.float32: "fp32", torch.float16: "fp16", torch.bfloat16: "bf16"}
@@ -87,6 +87,30 @@ def test_stage5_full_tile_counts(n, d, dtype, make_qkv):
     q, k, v = make_qkv(1, 3, n, d, dtype=dtype, device="cuda")
     o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=False)
     check_against_reference(o, q, k, v, False, dtype, lse=lse)
+
+
+# Stage 5 picks its workgroup height from the grid when no BR is forced: the tallest of 128 / 64 /
+# 32 rows that still gives every compute unit a workgroup. Each 32-row wave runs the same key split
+# and key order at every height, so the default must equal every forced height bit for bit. The
+# shapes are small grids (the default is BR 32 or 64 there) with N an odd multiple of 32, so the
+# forced BR = 64 / 128 runs also cover partial query tiles.
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("b,h,n,d", [(1, 3, 96, 64), (2, 4, 224, 64), (1, 16, 512, 128),
+                                     (2, 3, 352, 128)], ids=lambda x: str(x))
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=_pair_id)
+def test_stage5_default_height_matches_forced_heights(b, h, n, d, dtype, causal, make_qkv,
+                                                      reset_overrides):
+    require(5, dtype, d)
+    q, k, v = make_qkv(b, h, n, d, dtype=dtype, device="cuda", seed=5)
+    fused_attn.set_debug_overrides(0, 0)
+    o0, lse0 = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
+    check_against_reference(o0, q, k, v, causal, dtype, lse=lse0)
+    for br in (128, 64, 32):
+        fused_attn.set_debug_overrides(br, 0)
+        o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
+        torch.cuda.synchronize()
+        assert torch.equal(o, o0) and torch.equal(lse, lse0), f"BR = {br} differs from the default"
+    fused_attn.set_debug_overrides(0, 0)
 
 
 @pytest.mark.parametrize("stage", [1, 2])
