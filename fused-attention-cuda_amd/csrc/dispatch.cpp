@@ -267,10 +267,20 @@ constexpr int kDefaultBcF32 = 32;
 // N = 1024 26.8 -> 21.3 us (BR 64); at N = 2048 and above BR 128 stays the fastest. Heights
 // whose (BR, BC) pair is not instantiated are passed over. Each 32-row wave computes its rows
 // with the same key split and key order at every height, so the choice does not change results.
+//
+// Short key walks take BR 64 as well: when a 128-row workgroup would average fewer than 8 key
+// tiles (causal: about half of N / BC), its fixed cost (the first memory round trip, the key-split
+// merge, the epilogue) is a large share of it, and 64-row workgroups (4 waves, two per CU, no
+// shared barrier) overlap one workgroup's fixed cost with another's steps. Measured: the GPT-2
+// attention shape (B8 H12 N1024 D64 fp16 causal, 4.5 tiles on average) 43.1 -> 37.3 us, while
+// C64 (16 tiles) stays faster at BR 128 (29.3 against 30.6 us).
 int auto_br_s5(VariantList list, const fa_params& p, int bc) {
   const long long cus = current_device_cus();
+  const long long tiles = (p.N + bc - 1) / bc;
+  const bool short_walk = (p.causal ? tiles + 1 : 2 * tiles) < 16;  // twice the average
   for (const int br : {128, 64}) {
     if (find_variant(list, p.D, br, bc) == nullptr) continue;
+    if (br == 128 && short_walk && find_variant(list, p.D, 64, bc) != nullptr) continue;
     const long long grid = static_cast<long long>(p.B) * p.H * ((p.N + br - 1) / br);
     if (grid >= cus) return br;
   }
