@@ -19,7 +19,8 @@ Printed: ONE JSON line with the contract fields, plus
   over the same workload, repeated for a bounded budget of CPU time;
 * ``configs``: the other BASELINE configurations measured the same way (C128, C128 causal, LONG
   with its N sweep 512 / 1024 / 4096 / 8192, GPT attention shape), each with ms and TFLOP/s
-  (graph replay) and ``eager_ms``;
+  (graph replay) and ``eager_ms``, plus one GPU's share of 8-GPU layouts (C64 and LONG split
+  over heads, one ring step of LONG split over the sequence);
 * ``vendor_sdpa``: torch's ``scaled_dot_product_attention`` on the same inputs (fp16 configs);
 * ``protocol``: the reference's timing protocol (ref:docs/BENCHMARK_PROTOCOL.md rules 1-2) on the
   headline workload: 1 GiB flush before every launch, one event pair per launch, median/p10/p90.
@@ -56,6 +57,12 @@ WORKLOADS = {
     "LONG_N512": (1, 16, 512, 128, "bf16", True, 0.5),
     "LONG_N1024": (1, 16, 1024, 128, "bf16", True, 0.5),
     "LONG_N4096": (1, 16, 4096, 128, "bf16", True, 0.5),
+    # One GPU's share on 8 GPUs (no collective runs here): C64 and LONG split over heads (2 of
+    # their 16 each), and one ring step of LONG split over the sequence instead (1024 local
+    # queries against one unmasked 1024-key block).
+    "C64_heads8": (2, 1, 2048, 64, "fp16", False, 1.0),
+    "LONG_heads8": (1, 2, 8192, 128, "bf16", True, 0.5),
+    "LONG_ring8": (1, 16, 1024, 128, "bf16", False, 0.5),
 }
 
 
@@ -85,11 +92,28 @@ def make_inputs(torch, b, h, n, d, dtype, std, seed):
                  for _ in range(3))
 
 
+# Workspace per output buffer (o.data_ptr() -> tensor), allocated once per input set before any
+# timing or graph capture: stage 5 takes one (fa_workspace_bytes) where it splits key walks.
+_WORKSPACE = {}
+
+
+def attach_workspaces(torch, capi, sets, causal, scale, stage):
+    for q, k, _, o, _ in sets:
+        nbytes = capi.workspace_bytes(stage, q, k, causal, scale)
+        _WORKSPACE[o.data_ptr()] = (torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+                                    if nbytes else None)
+
+
+def workspace_of(o):
+    return _WORKSPACE.get(o.data_ptr())
+
+
 def gate(torch, capi, q, k, v, o, lse, causal, scale, stage, stream):
     """Correctness gate before timing: selected rows of two heads vs the fp64 oracle."""
     from oracle.oracle import math_reference_rows
 
-    rc = capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream)
+    rc = capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream,
+                      workspace=workspace_of(o))
     if rc != 0:
         raise RuntimeError(f"fa_forward failed: {capi.error_string(rc)}")
     stream.synchronize()
@@ -124,7 +148,9 @@ def time_steps(torch, capi, args_list, causal, scale, stage, stream, steps, warm
         b, h, n, d = q.shape
         p = capi.params(b, h, k.shape[1], n, d, scale, causal)
         calls.append((stage, capi.DTYPE_CODES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                      o.data_ptr(), lse.data_ptr(), None, ctypes.byref(p), stream.cuda_stream, p))
+                      o.data_ptr(), lse.data_ptr(),
+                      None if workspace_of(o) is None else workspace_of(o).data_ptr(),
+                      ctypes.byref(p), stream.cuda_stream, p))
     fwd = lib.fa_forward
 
     def launch(c):
@@ -153,14 +179,16 @@ def graph_timing(torch, capi, args_list, causal, scale, stage, stream, steps):
     eager launch per input set (the kernel is deterministic). Returns ms per launch."""
     with torch.cuda.stream(stream):  # one eager launch per set: the reference outputs
         for q, k, v, o, lse in args_list:
-            capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream)
+            capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream,
+                         workspace=workspace_of(o))
     stream.synchronize()
     eager = [(o.clone(), lse.clone()) for _, _, _, o, lse in args_list]
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
         for i in range(steps):
             q, k, v, o, lse = args_list[i % len(args_list)]
-            capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream)
+            capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream,
+                         workspace=workspace_of(o))
     for _ in range(2):
         for _, _, _, o, lse in args_list:
             o.zero_()
@@ -193,7 +221,8 @@ def protocol_timing(torch, capi, args_list, causal, scale, stage, stream, iters=
             flush.zero_()
             q, k, v, o, lse = args_list[i % len(args_list)]
             evs[i][0].record(stream)
-            capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream)
+            capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream,
+                         workspace=workspace_of(o))
             evs[i][1].record(stream)
     stream.synchronize()
     ms = sorted(a.elapsed_time(b) for a, b in evs)
@@ -261,6 +290,7 @@ def bench_workload(torch, capi, name, stage, steps, warmup, seed=0, gate_it=True
             o = torch.empty_like(q)
             lse = torch.empty(b, h, n, dtype=torch.float32, device="cuda")
             sets.append((q, k, v, o, lse))
+    attach_workspaces(torch, capi, sets, causal, scale, stage)
     stream.synchronize()
     err = gate(torch, capi, *sets[0], causal, scale, stage, stream) if gate_it else (None, None)
     eager_ms = time_steps(torch, capi, sets, causal, scale, stage, stream,
@@ -272,6 +302,9 @@ def bench_workload(torch, capi, name, stage, steps, warmup, seed=0, gate_it=True
            "ms": ms, "tflops": tf, "pct_peak": 100.0 * tf / PEAK_TFLOPS[dt], "flops": f,
            "eager_ms": eager_ms if eager else None, "gate_max_err_o": err[0],
            "gate_max_err_lse": err[1]}
+    # Split key walks (stage 5 with a workspace): S parts of fp32 O and LSE per row.
+    ws = workspace_of(sets[0][3])
+    res["splits"] = 1 if ws is None else max(1, ws.numel() // (b * h * n * (d + 1) * 4))
     return res, sets, stream, causal, scale
 
 
@@ -415,7 +448,8 @@ def main(argv=None) -> int:
                                f"{'causal' if causal else 'non-causal'}, stage {a.stage} "
                                f"(fa_s5_tuned)" if a.stage == 5 else
                                f"{a.workload}: B{b} H{h} N{n} D{d} {dt} stage {a.stage}",
-                   "B": b, "H": h, "N": n, "D": d, "causal": causal, "stage": a.stage},
+                   "B": b, "H": h, "N": n, "D": d, "causal": causal, "stage": a.stage,
+                   "splits": head["splits"]},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
                      "peak": PEAK_TFLOPS[dt], "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS[dt], 5),

@@ -540,8 +540,14 @@ struct Fa16 {
     const int rem = G % kNumXcd;
     const int logical =
         (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + bid / kNumXcd;
-    const int bh = logical / a.n_qtiles;
-    int qt = logical - bh * a.n_qtiles;
+    // With split key walks the n_splits parts of one query tile are consecutive items.
+    // (readfirstlane: uniform integer divisions run on the vector unit, and their results would
+    // otherwise occupy vector registers for the whole kernel.)
+    const int S = a.n_splits;
+    const int item = __builtin_amdgcn_readfirstlane(S > 1 ? logical / S : logical);
+    const int part = logical - item * S;
+    const int bh = item / a.n_qtiles;
+    int qt = item - bh * a.n_qtiles;
     if (a.causal) qt = a.n_qtiles - 1 - qt;  // longest key ranges first
     const int b = bh / a.H;
     const int h = bh - b * a.H;
@@ -556,9 +562,12 @@ struct Fa16 {
     const int r0 = i0 + 32 * rg;  // this wave's first row
     const bool wave_valid = r0 < N;
     const int row = r0 + (lane & 31);
-    // Key range of the workgroup (causal stops at its last row) and of this wave.
+    // Key range of the workgroup (causal stops at its last row) and of this wave. The workgroup
+    // walks key tiles [t0, n_tiles): the whole walk, or its part of a split walk.
     const int kv_end = a.causal ? min(N, i0 + kBr) : N;
-    const int n_tiles = (kv_end + BC - 1) / BC;
+    const int n_walk = (kv_end + BC - 1) / BC;
+    const int t0 = __builtin_amdgcn_readfirstlane(part * n_walk / S);
+    const int n_tiles = __builtin_amdgcn_readfirstlane((part + 1) * n_walk / S);
     const int wave_end = wave_valid ? (a.causal ? min(N, r0 + 32) : N) : 0;
     const int kbase = ks * BCW;  // this wave's keys inside every tile
     const float c = a.c;
@@ -596,19 +605,20 @@ struct Fa16 {
 
     Probs P;
     if constexpr (PIPE) {
+     if (t0 < n_tiles) {  // workgroup-uniform: an empty part of a split walk loads nothing
       // Software pipeline: iteration t exponentiates tile t while the MFMAs of S(t+1) = K(t+1) Q^T
-      // run, then applies P(t) to V(t). K is therefore staged one tile ahead of V: iteration t
-      // reads K buffer (t+1)%2 and V buffer t%2 and refills K buffer t%2 with K(t+2) and V buffer
-      // (t+1)%2 with V(t+1), each loaded into registers at the top of the iteration.
-      // K(0), V(0) and K(1) in flight together (one memory round trip for the prologue).
-      dma_tile<false>(kbuf0, kg, dk, 0, N, ksn, wave);
-      dma_tile<true>(vbuf0, vg, dv, 0, N, vsn, wave);
-      if (n_tiles > 1) dma_tile<false>(kbuf0 + kKElems, kg, dk, BC, N, ksn, wave);
+      // run, then applies P(t) to V(t). K is therefore staged one tile ahead of V: with u = t - t0,
+      // iteration t reads K buffer (u+1)%2 and V buffer u%2 and refills K buffer u%2 with K(t+2)
+      // and V buffer (u+1)%2 with V(t+1).
+      // K(t0), V(t0) and K(t0+1) in flight together (one memory round trip for the prologue).
+      dma_tile<false>(kbuf0, kg, dk, t0 * BC, N, ksn, wave);
+      dma_tile<true>(vbuf0, vg, dv, t0 * BC, N, vsn, wave);
+      if (t0 + 1 < n_tiles) dma_tile<false>(kbuf0 + kKElems, kg, dk, (t0 + 1) * BC, N, ksn, wave);
       wait_dma();
       __syncthreads();
       f32x16 sa[kKB], sb[kKB];
       {
-        const int nv0 = nvalid_of(0);
+        const int nv0 = nvalid_of(t0);
         if (nv0 > 0) qk<false>(sa, ws, kwave(0), nv0, kl);
       }
       __syncthreads();  // K buffer 0 is refilled in iteration 0
@@ -617,14 +627,15 @@ struct Fa16 {
       // no per-block branches and the VALU softmax of S(t) interleaves with the MFMAs of S(t+1).
       // The parity tag makes the calls with swapped S arrays distinct instantiations (one function
       // called with swapped arrays gets its calls merged through pointer phis, which pins the
-      // arrays in scratch memory).
+      // arrays in scratch memory). It is also the parity of u = t - t0 (every call below passes
+      // P0 at even u), so each call's LDS buffers are compile-time choices.
       auto iter = [&](auto full, auto parity, int t, f32x16(&s_cur)[kKB],
                       f32x16(&s_nxt)[kKB]) __attribute__((always_inline)) {
-        (void)parity;
         constexpr bool kFull = decltype(full)::value;
+        constexpr int u = decltype(parity)::value;  // (t - t0) & 1
         // K(t+2) and V(t+1) go straight into the buffers this iteration does not read.
-        const T* kn = kwave((t + 1) & 1);
-        const T* vc = vwave(t & 1);
+        const T* kn = kwave((u + 1) & 1);
+        const T* vc = vwave(u & 1);
         if constexpr (kFull) {
           // The tiles loaded are clamped to the last one: past the end of the key range (the last
           // two steps when every tile is full) the copies land in buffers that are not read again
@@ -632,14 +643,14 @@ struct Fa16 {
           // the tail on this branch-free body.
           const int tk = min(t + 2, n_tiles - 1), tv = min(t + 1, n_tiles - 1);
           step_full(ws, s_cur, s_nxt, P, kn, vc, kl, vl, c, lane, [&] {
-            dma_tile_full<false>(kbuf0 + (t & 1) * kKElems, kg, dk, tk * BC, ksn, wave);
-            dma_tile_full<true>(vbuf0 + ((t + 1) & 1) * kVElems, vg, dv, tv * BC, vsn, wave);
+            dma_tile_full<false>(kbuf0 + (u & 1) * kKElems, kg, dk, tk * BC, ksn, wave);
+            dma_tile_full<true>(vbuf0 + ((u + 1) & 1) * kVElems, vg, dv, tv * BC, vsn, wave);
           });
         } else {
           // LDS-DMA from inline assembly: the compiler would otherwise make the LDS reads below
           // wait for these loads, which target buffers this iteration does not read.
-          if (t + 2 < n_tiles) dma_tile_asm<false>(kbuf0 + (t & 1) * kKElems, kg, dk, (t + 2) * BC, N, ksn, wave);
-          if (t + 1 < n_tiles) dma_tile_asm<true>(vbuf0 + ((t + 1) & 1) * kVElems, vg, dv, (t + 1) * BC, N, vsn, wave);
+          if (t + 2 < n_tiles) dma_tile_asm<false>(kbuf0 + (u & 1) * kKElems, kg, dk, (t + 2) * BC, N, ksn, wave);
+          if (t + 1 < n_tiles) dma_tile_asm<true>(vbuf0 + ((u + 1) & 1) * kVElems, vg, dv, (t + 1) * BC, N, vsn, wave);
           const int nv = nvalid_of(t);
           const int dg = diag_of(t, nv);
           const int nv_nxt = (t + 1 < n_tiles) ? nvalid_of(t + 1) : 0;
@@ -659,16 +670,17 @@ struct Fa16 {
       using P0 = std::integral_constant<int, 0>;
       using P1 = std::integral_constant<int, 1>;
       // Tiles [0, n_full) are full for every wave and carry no diagonal (workgroup-uniform): key
-      // tile t is complete below the workgroup's first row (causal) or below N. When every tile is
-      // full (non-causal, N a multiple of BC) all of them take the steady step; otherwise steady
-      // step t also needs tile t+1 full and K(t+2) a whole tile inside the tensor
-      // (t + 3 <= N / BC), so that its loads need no clamp.
+      // tile t is complete below the workgroup's first row (causal) or below N. When every tile of
+      // [t0, n_tiles) is full all of them take the steady step; otherwise steady step t also needs
+      // tile t+1 full and K(t+2) a whole tile inside the tensor (t + 3 <= N / BC), so that its
+      // loads need no clamp. Steady steps are t in [t0, n_steady).
       const int n_full = (a.causal ? i0 : N) / BC;
-      const int n_steady = n_full >= n_tiles ? n_tiles
-                                             : max(0, min(min(n_tiles, n_full) - 1, N / BC - 2));
+      const int n_steady = n_full >= n_tiles
+                               ? n_tiles
+                               : max(t0, min(min(n_tiles, n_full) - 1, N / BC - 2));
       // Unrolled by two so the S(t) / S(t+1) register sets swap roles without copies; the steady
       // loop and the tail loop get independent register assignments.
-      int t = 0;
+      int t = t0;
       for (; t + 1 < n_steady; t += 2) {
         iter(Full{}, P0{}, t, sa, sb);
         iter(Full{}, P1{}, t + 1, sb, sa);
@@ -683,9 +695,10 @@ struct Fa16 {
         iter(Part{}, P0{}, t, sa, sb);
         if (t + 1 < n_tiles) iter(Part{}, P1{}, t + 1, sb, sa);
       }
+     }
     } else {
       f32x16 s[kKB];
-      for (int t = 0; t < n_tiles; ++t) {
+      for (int t = t0; t < n_tiles; ++t) {
         dma_tile<false>(kbuf0, kg, dk, t * BC, N, ksn, wave);
         dma_tile<true>(vbuf0, vg, dv, t * BC, N, vsn, wave);
         wait_dma();
@@ -743,6 +756,29 @@ struct Fa16 {
     const float lt = ws.l + __shfl_xor(ws.l, 32);
     if (!wave_valid) return;
     const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
+    if (S > 1) {
+      // One part of a split walk: its normalised O in fp32 and its LSE (-inf when the part saw
+      // no key) for fa_s5_combine.
+      const size_t prow =
+          ((static_cast<size_t>(part) * a.B + b) * a.H + h) * static_cast<size_t>(N) + row;
+      float* op = a.o_part + prow * D;
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d = 32 * db + 8 * j + 4 * g;
+          *reinterpret_cast<float4*>(op + d) =
+              float4{ws.o[db][4 * j + 0] * inv, ws.o[db][4 * j + 1] * inv,
+                     ws.o[db][4 * j + 2] * inv, ws.o[db][4 * j + 3] * inv};
+        }
+      }
+      if (g == 0) {
+        a.lse_part[prow] = (lt > 0.f && ws.m != -__builtin_inff())
+                               ? ws.m * a.scale + log2_hw(lt) * kLn2
+                               : -__builtin_inff();
+      }
+      return;
+    }
     T* orow = static_cast<T*>(a.o) + b * a.osb + h * a.osh + row * a.osn;
 #pragma unroll
     for (int db = 0; db < kDB; ++db) {
@@ -778,13 +814,77 @@ __global__ __launch_bounds__(64 * RG * KS) void fa_s4_mfma(KArgs a) {
   Fa16<T, D, RG, KS, BCW, false>::run(a);
 }
 
+// Merge of the parts of split key walks: per row, L* = max_s LSE_s, w_s = exp(LSE_s - L*),
+// O = sum_s w_s O_s / sum_s w_s and LSE = L* + ln sum_s w_s (the log-sum-exp merge of partial
+// softmax states, ref:include/fa/softmax_math.cuh:65-68; empty parts carry LSE_s = -inf and weigh
+// nothing). One thread per four head-dim elements of a row; fp32 throughout, one rounding to T.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void fa_s5_combine(KArgs a) {
+  constexpr int kTpr = D / 4;  // threads per row
+  constexpr int kRows = 256 / kTpr;
+  constexpr float kLog2e = 1.44269504088896341f;
+  const long long rows = static_cast<long long>(a.B) * a.H * a.N;
+  const long long r = static_cast<long long>(blockIdx.x) * kRows + threadIdx.x / kTpr;
+  if (r >= rows) return;
+  const int d = 4 * (threadIdx.x % kTpr);
+  const int S = a.n_splits;
+  float lmax = -__builtin_inff();
+  for (int sp = 0; sp < S; ++sp) lmax = fmaxf(lmax, a.lse_part[sp * rows + r]);
+  const long long bh = r / a.N;
+  const int n = static_cast<int>(r - bh * a.N);
+  const int b = static_cast<int>(bh / a.H);
+  const int h = static_cast<int>(bh - static_cast<long long>(b) * a.H);
+  T* orow = static_cast<T*>(a.o) + b * a.osb + h * a.osh + static_cast<long long>(n) * a.osn + d;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float sum = 0.f;
+  if (lmax != -__builtin_inff()) {
+    for (int sp = 0; sp < S; ++sp) {
+      const float w = exp2_hw((a.lse_part[sp * rows + r] - lmax) * kLog2e);
+      const float4 v = *reinterpret_cast<const float4*>(a.o_part + (sp * rows + r) * D + d);
+      sum += w;
+      acc[0] = __builtin_fmaf(w, v.x, acc[0]);
+      acc[1] = __builtin_fmaf(w, v.y, acc[1]);
+      acc[2] = __builtin_fmaf(w, v.z, acc[2]);
+      acc[3] = __builtin_fmaf(w, v.w, acc[3]);
+    }
+  }
+  // A row no part saw (impossible for a non-empty walk) keeps O = 0 and LSE = +inf.
+  const float inv = sum > 0.f ? 1.f / sum : 0.f;
+  if constexpr (__is_same(T, _Float16)) {
+    *reinterpret_cast<f16x4*>(orow) = f16x4{(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv),
+                                            (_Float16)(acc[2] * inv), (_Float16)(acc[3] * inv)};
+  } else {
+    *reinterpret_cast<bf16x4*>(orow) = bf16x4{(__bf16)(acc[0] * inv), (__bf16)(acc[1] * inv),
+                                              (__bf16)(acc[2] * inv), (__bf16)(acc[3] * inv)};
+  }
+  if (d == 0) a.lse[r] = sum > 0.f ? lmax + log2_hw(sum) * kLn2 : __builtin_inff();
+}
+
+template <typename T, int D>
+int launch_combine(const KArgs& a, hipStream_t stream) {
+  constexpr int kRows = 256 / (D / 4);
+  const long long rows = static_cast<long long>(a.B) * a.H * a.N;
+  const long long grid = (rows + kRows - 1) / kRows;
+  if (a.n_splits < 2 || a.o_part == nullptr || a.lse_part == nullptr || grid <= 0 ||
+      grid > 0x7fffffffLL) {
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  hipLaunchKernelGGL((fa_s5_combine<T, D>), dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                     stream, a);
+  return static_cast<int>(hipGetLastError());
+}
+
 // Host-side launch of one instantiated variant (STAGE 5 or 4).
 template <int STAGE, typename T, int D, int RG, int KS, int BCW>
 int launch(const KArgs& in, hipStream_t stream) {
   using A = Fa16<T, D, RG, KS, BCW, STAGE == 5>;
   KArgs a = in;
   a.n_qtiles = (a.N + A::kBr - 1) / A::kBr;
-  const long long grid = static_cast<long long>(a.n_qtiles) * a.B * a.H;
+  if (a.n_splits < 1 || (a.n_splits > 1 && (STAGE != 5 || a.o_part == nullptr ||
+                                            a.lse_part == nullptr))) {
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  const long long grid = static_cast<long long>(a.n_qtiles) * a.B * a.H * a.n_splits;
   if (grid <= 0 || grid > 0x7fffffffLL) return static_cast<int>(hipErrorInvalidValue);
   const dim3 gr(static_cast<unsigned>(grid)), bl(A::kThreads);
   if constexpr (STAGE == 5) {

@@ -197,6 +197,9 @@ KArgs make_args(const void* q, const void* k, const void* v, void* o, float* lse
   a.osb = st.o.b;
   a.osh = st.o.h;
   a.osn = static_cast<int>(st.o.n);
+  a.n_splits = 1;
+  a.o_part = nullptr;
+  a.lse_part = nullptr;
   return a;
 }
 
@@ -287,6 +290,76 @@ int auto_br_s5(VariantList list, const fa_params& p, int bc) {
   return find_variant(list, p.D, 32, bc) != nullptr ? 32 : kDefaultBr;
 }
 
+VariantList s5_list(int dtype) {
+  return dtype == FA_DTYPE_F16 ? variants_s5_f16() : variants_s5_bf16();
+}
+
+// Split key walks (stage 5, with a workspace). When the grid leaves CUs idle, or a causal
+// problem's longest key walk is far above the average work per CU, the critical path is one
+// workgroup's walk. Cutting every walk into S parts of whole tiles (one workgroup each; the parts'
+// normalised fp32 O and LSE are merged by fa_s5_combine) shortens it to about 1/S, at the price
+// of more workgroups (each with its fixed cost) and of the combine's traffic. The model, in
+// microseconds with one key-tile step ~ 1 us and a workgroup's fixed cost ~ 2.5 steps:
+//   time(S)  = max(ceil(longest walk / S) + fixed, (all steps + workgroups(S) * fixed) / CUs)
+//              + (S > 1 ? combine : 0)
+//   combine  = (2 S + 0.5) * rows * D * 4 bytes at 4 TB/s (the parts written, read back, and O)
+//              + 2 us for the second launch.
+// The S in 2..16 with the least time is taken when it saves at least 20 % over S = 1. On MI355X
+// this splits the shapes of one GPU's share of a head-sharded problem (C64's 2 heads of 16,
+// LONG's 2 of 16) and leaves every BASELINE configuration whole. FA_FORCE_SPLITS (test-only)
+// forces S; fa_workspace_bytes and fa_forward must see the same value.
+constexpr int kMaxSplits = 16;
+int s5_splits(const fa_params& p, int dtype) {
+  if (const int f = env_positive_int("FA_FORCE_SPLITS")) return std::min(f, kMaxSplits);
+  if (p.B < 1 || p.H < 1 || p.N < 1) return 1;
+  const int bc = default_bc_mfma(p.D);
+  const int br = auto_br_s5(s5_list(dtype), p, bc);
+  const double cus = static_cast<double>(current_device_cus());
+  const long long n_qt = (p.N + br - 1) / br;
+  const long long longest = (p.N + bc - 1) / bc;
+  long long steps_per_head = 0;
+  if (p.causal) {
+    for (long long qt = 0; qt < n_qt; ++qt) {
+      steps_per_head += (std::min<long long>(p.N, (qt + 1) * br) + bc - 1) / bc;
+    }
+  } else {
+    steps_per_head = n_qt * longest;
+  }
+  const double heads = static_cast<double>(p.B) * p.H;
+  const double steps = heads * static_cast<double>(steps_per_head);
+  const double rows = heads * p.N;
+  constexpr double kFixed = 2.5, kBytesPerUs = 4.0e6, kLaunchUs = 2.0;
+  auto time = [&](int S) {
+    const double part = static_cast<double>((longest + S - 1) / S);
+    const double wgs = heads * static_cast<double>(n_qt) * S;
+    double t = std::max(part + kFixed, (steps + wgs * kFixed) / cus);
+    if (S > 1) t += (2.0 * S + 0.5) * rows * p.D * 4.0 / kBytesPerUs + kLaunchUs;
+    return t;
+  };
+  const double whole = time(1);
+  int best = 1;
+  double best_t = whole;
+  for (int S = 2; S <= kMaxSplits && S <= longest; ++S) {
+    const double t = time(S);
+    if (t < best_t) {
+      best_t = t;
+      best = S;
+    }
+  }
+  return best_t <= 0.8 * whole ? best : 1;
+}
+
+// Workspace of a split launch: the parts' fp32 O [S, B, H, N, D], then their LSE [S, B, H, N].
+size_t s5_opart_bytes(const fa_params& p, int splits) {
+  const size_t rows = static_cast<size_t>(p.B) * p.H * p.N;
+  return (static_cast<size_t>(splits) * rows * p.D * sizeof(float) + 255) / 256 * 256;
+}
+size_t s5_workspace_bytes(const fa_params& p, int splits) {
+  if (splits < 2) return 0;
+  const size_t rows = static_cast<size_t>(p.B) * p.H * p.N;
+  return s5_opart_bytes(p, splits) + static_cast<size_t>(splits) * rows * sizeof(float);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------------------------
@@ -298,16 +371,31 @@ bool supports(int dtype, int D, int arch) {
 }
 
 int forward(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
-            const fa_params& p, const Strides& st, const Overrides& dbg, int arch,
-            hipStream_t stream) {
+            void* workspace, const fa_params& p, const Strides& st, const Overrides& dbg,
+            int arch, hipStream_t stream) {
   if (!supports(dtype, p.D, arch)) return static_cast<int>(hipErrorNotSupported);
   const int rc = common_stage_checks("stage5", q, k, v, o, lse, p);
   if (rc != 0) return rc;
   const int bc = dbg.block_n != 0 ? dbg.block_n : default_bc_mfma(p.D);
-  const KArgs a = make_args(q, k, v, o, lse, p, st);
-  const VariantList list = dtype == FA_DTYPE_F16 ? variants_s5_f16() : variants_s5_bf16();
+  KArgs a = make_args(q, k, v, o, lse, p, st);
+  const VariantList list = s5_list(dtype);
   const int br = dbg.block_m != 0 ? dbg.block_m : auto_br_s5(list, p, bc);
-  return launch_selected("stage5", list, br, bc, a, p.D, stream);
+  // With a workspace (fa_workspace_bytes > 0) the key walks may be split; without one the
+  // whole-walk kernel runs.
+  const int splits = workspace != nullptr ? s5_splits(p, dtype) : 1;
+  if (splits < 2) return launch_selected("stage5", list, br, bc, a, p.D, stream);
+  if (!aligned16(workspace)) {
+    if (verbose()) std::fprintf(stderr, "fa::stage5: workspace must be 16-byte aligned\n");
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  const LaunchFn combine = dtype == FA_DTYPE_F16 ? combine_s5_f16(p.D) : combine_s5_bf16(p.D);
+  if (combine == nullptr) return static_cast<int>(hipErrorNotSupported);
+  a.n_splits = splits;
+  a.o_part = static_cast<float*>(workspace);
+  a.lse_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + s5_opart_bytes(p, splits));
+  const int lrc = launch_selected("stage5", list, br, bc, a, p.D, stream);
+  if (lrc != 0) return lrc;
+  return combine(a, stream);
 }
 }  // namespace stage5
 
@@ -318,8 +406,8 @@ namespace stage4 {
 bool supports(int dtype, int D, int arch) { return stage5::supports(dtype, D, arch); }
 
 int forward(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
-            const fa_params& p, const Strides& st, const Overrides& dbg, int arch,
-            hipStream_t stream) {
+            void* workspace, const fa_params& p, const Strides& st, const Overrides& dbg,
+            int arch, hipStream_t stream) {
   if (!supports(dtype, p.D, arch)) return static_cast<int>(hipErrorNotSupported);
   const int rc = common_stage_checks("stage4", q, k, v, o, lse, p);
   if (rc != 0) return rc;
@@ -344,8 +432,8 @@ bool supports(int dtype, int D, int arch) {
 }
 
 int forward(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
-            const fa_params& p, const Strides& st, const Overrides& dbg, int arch,
-            hipStream_t stream) {
+            void* workspace, const fa_params& p, const Strides& st, const Overrides& dbg,
+            int arch, hipStream_t stream) {
   if (!supports(dtype, p.D, arch)) return static_cast<int>(hipErrorNotSupported);
   const int rc = common_stage_checks("stage3", q, k, v, o, lse, p);
   if (rc != 0) return rc;
@@ -379,11 +467,12 @@ int forward_impl(int impl, int dtype, const void* q, const void* k, const void* 
     }
     return static_cast<int>(hipErrorNotSupported);
   }
-  if (fa_workspace_bytes(impl, dtype, p) > 0 && workspace == nullptr) {
+  // Stage 5's workspace is optional (split key walks); the materialising stages need theirs.
+  if (impl != FA_IMPL_TUNED && fa_workspace_bytes(impl, dtype, p) > 0 && workspace == nullptr) {
     if (fa::verbose()) std::fprintf(stderr, "fa_forward: workspace required but NULL\n");
     return static_cast<int>(hipErrorInvalidValue);
   }
-  return e->forward(dtype, q, k, v, o, lse, *p, st, fa::overrides_now(), arch, stream);
+  return e->forward(dtype, q, k, v, o, lse, workspace, *p, st, fa::overrides_now(), arch, stream);
 }
 }  // namespace
 }  // namespace fa
@@ -547,9 +636,16 @@ int fa_forward_strided(int impl, int dtype, const void* q, const fa_strides* q_s
   return fa::forward_impl(impl, dtype, q, k, v, o, lse, workspace, p, st, stream);
 }
 
-size_t fa_workspace_bytes(int impl, int /*dtype*/, const fa_params* p) {
-  // Materialising stages keep fp32 S and P (ref:src/dispatch.cu:163-168); fused stages need none.
-  if (p == nullptr || (impl != FA_IMPL_NAIVE && impl != FA_IMPL_TILED)) return 0;
+size_t fa_workspace_bytes(int impl, int dtype, const fa_params* p) {
+  // Materialising stages keep fp32 S and P (ref:src/dispatch.cu:163-168). Stage 5 takes an
+  // optional workspace for split key walks (fp32 partial O and LSE) on problems that leave the
+  // GPU underused; the other fused stages need none.
+  if (p == nullptr) return 0;
+  if (impl == FA_IMPL_TUNED) {
+    if ((dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16) || (p->D != 64 && p->D != 128)) return 0;
+    return fa::s5_workspace_bytes(*p, fa::s5_splits(*p, dtype));
+  }
+  if (impl != FA_IMPL_NAIVE && impl != FA_IMPL_TILED) return 0;
   const size_t n = static_cast<size_t>(p->N);
   return 2u * static_cast<size_t>(p->B) * static_cast<size_t>(p->H) * n * n * sizeof(float);
 }

@@ -42,6 +42,13 @@ struct KArgs {
   // always dense [B, H, N].
   long long qsb, qsh, ksb, ksh, vsb, vsh, osb, osh;
   int qsn, ksn, vsn, osn;
+  // Split key walks (stage 5): with n_splits > 1 every query tile's key walk is cut into
+  // n_splits parts of whole tiles, one workgroup each, and each part writes its normalised fp32
+  // partial O to o_part [n_splits, B, H, N, D] and its LSE to lse_part [n_splits, B, H, N]
+  // (-inf for an empty part); fa_s5_combine then writes o and lse. n_splits = 1: no split.
+  int n_splits;
+  float* o_part;
+  float* lse_part;
 };
 
 // Arguments of the split-KV decode kernels (attn_decode.h). q, o: [B, H, Nq, D]; k, v:
@@ -90,22 +97,25 @@ VariantList variants_s5_bf16();  // attn_bf16.hip
 VariantList variants_s4_bf16();  // attn_bf16.hip
 VariantList variants_s3_f32();   // attn_f32.hip (fp32 I/O)
 VariantList variants_s3_f16();   // attn_f32.hip (fp16 I/O, fp32 compute)
+LaunchFn combine_s5_f16(int D);   // attn_f16.hip: fa_s5_combine (split key walks); nullptr: no D
+LaunchFn combine_s5_bf16(int D);  // attn_bf16.hip
 
 // Strides of the four [B, H, N, D] operands (fa_strides of include/fa/attention.h).
 struct Strides {
   fa_strides q, k, v, o;
 };
 
+// `workspace` is the caller's fa_forward workspace (may be null; see fa_workspace_bytes).
 using StageForwardFn = int (*)(int dtype, const void* q, const void* k, const void* v, void* o,
-                               float* lse, const fa_params& p, const Strides& st,
+                               float* lse, void* workspace, const fa_params& p, const Strides& st,
                                const Overrides& dbg, int arch, hipStream_t stream);
 using StageSupportsFn = bool (*)(int dtype, int D, int arch);
 
 #define FA_DECLARE_STAGE(ns)                                                                   \
   namespace ns {                                                                               \
   int forward(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,     \
-              const fa_params& p, const Strides& st, const Overrides& dbg, int arch,           \
-              hipStream_t stream);                                                             \
+              void* workspace, const fa_params& p, const Strides& st, const Overrides& dbg,    \
+              int arch, hipStream_t stream);                                                   \
   bool supports(int dtype, int D, int arch);                                                   \
   }
 FA_DECLARE_STAGE(stage3)  // attn_f32.hip   fa_s3_fused  : fp32 MFMA compute, fp32/fp16 I/O

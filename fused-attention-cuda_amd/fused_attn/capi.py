@@ -128,16 +128,31 @@ def forward_raw(impl: int, dtype: int, q: int, k: int, v: int, o: int, lse: int,
     return load().fa_forward(impl, dtype, q, k, v, o, lse, workspace, ctypes.byref(p), stream)
 
 
+def workspace_bytes(impl: int, q: torch.Tensor, k: torch.Tensor, is_causal: bool,
+                    scale: float) -> int:
+    """``fa_workspace_bytes`` for these operands (stage 5: bytes that enable split key walks)."""
+    b, h, n, d = q.shape
+    p = params(b, h, k.shape[1], n, d, scale, is_causal)
+    return int(load().fa_workspace_bytes(impl, DTYPE_CODES.get(q.dtype, -1), ctypes.byref(p)))
+
+
 def forward(impl: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
             lse: torch.Tensor | None, is_causal: bool, scale: float,
-            stream: torch.cuda.Stream | None = None) -> int:
+            stream: torch.cuda.Stream | None = None,
+            workspace: torch.Tensor | None | str = "auto") -> int:
     """``fa_forward`` on torch device tensors (caller-allocated o and lse, like any C caller).
-    Launches on ``stream`` (default: torch's current stream) and returns the hipError_t value."""
+    Launches on ``stream`` (default: torch's current stream) and returns the hipError_t value.
+    ``workspace``: "auto" allocates the bytes ``fa_workspace_bytes`` asks for (none for most
+    problems), None passes a null workspace, a tensor is passed as is."""
     b, h, n, d = q.shape
     p = params(b, h, k.shape[1], n, d, scale, is_causal)
     s = stream if stream is not None else torch.cuda.current_stream(q.device)
+    if isinstance(workspace, str):
+        nbytes = workspace_bytes(impl, q, k, is_causal, scale)
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
+    ws = 0 if workspace is None else workspace.data_ptr()
     return forward_raw(impl, DTYPE_CODES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                       o.data_ptr(), 0 if lse is None else lse.data_ptr(), 0, p, s.cuda_stream)
+                       o.data_ptr(), 0 if lse is None else lse.data_ptr(), ws, p, s.cuda_stream)
 
 
 def strides_of(t: torch.Tensor) -> FaStrides:

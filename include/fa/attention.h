@@ -64,7 +64,10 @@ typedef struct fa_params {
 
 /* Replaces fa::forward (ref:include/fa/attention.cuh:46-47, ref:src/dispatch.cu:140-161).
  * Returns a hipError_t value. `lse` must be non-null for stages 3-5. `workspace` may be NULL when
- * fa_workspace_bytes() is 0 (always, for the stages this build implements). */
+ * fa_workspace_bytes() is 0. For stage 5 it is optional even then: with a 16-byte aligned
+ * workspace of fa_workspace_bytes() bytes (queried for the same params, dtype and environment)
+ * the key walks are split across workgroups and a second kernel merges the parts; with NULL the
+ * single-kernel path runs. A workspace must not be shared by launches that may overlap. */
 FA_API int fa_forward(int impl, int dtype, const void* q, const void* k, const void* v, void* o,
                float* lse, void* workspace, const fa_params* p, hipStream_t stream);
 
@@ -91,7 +94,10 @@ FA_API int fa_forward_strided(int impl, int dtype, const void* q, const fa_strid
                               hipStream_t stream);
 
 /* Replaces fa::workspace_bytes (ref:include/fa/attention.cuh:51, ref:src/dispatch.cu:163-168):
- * 2*B*H*N*N*4 for the materialising stages 1-2, 0 for the fused stages. */
+ * 2*B*H*N*N*4 for the materialising stages 1-2; 0 for stages 3-4; for stage 5, 0 or, where the
+ * library's cost model splits the key walks (problems that leave most of the GPU idle, such as
+ * one GPU's share of a head-sharded problem), the fp32 partial O and LSE of S parts:
+ * round_up(S*B*H*N*D*4, 256) + S*B*H*N*4 bytes. FA_FORCE_SPLITS (test-only) forces S <= 16. */
 FA_API size_t fa_workspace_bytes(int impl, int dtype, const fa_params* p);
 
 /* Replaces fa::impl_supports (ref:include/fa/attention.cuh:56, ref:src/dispatch.cu:170-175).

@@ -67,6 +67,41 @@ def test_workspace_bytes():
         assert lib.fa_workspace_bytes(impl, 1, p) == 0
 
 
+def _split_bytes(splits, rows, d):
+    opart = (splits * rows * d * 4 + 255) // 256 * 256
+    return opart + splits * rows * 4
+
+
+def test_stage5_split_workspace(monkeypatch):
+    """Stage 5 asks for a workspace (fp32 partial O [S, B, H, N, D] + LSE [S, B, H, N]) only where
+    its cost model splits the key walks. Without a device the model assumes 256 CUs (MI355X):
+    one GPU's share of C64 over 8 GPUs (B2 H1) and of LONG (B1 H2 N8192 causal) split in two,
+    the BASELINE configurations and the GPT-2 attention shape do not."""
+    monkeypatch.delenv("FA_FORCE_SPLITS", raising=False)
+    lib = capi.load()
+    f16, bf16 = capi.FA_DTYPE_F16, capi.FA_DTYPE_BF16
+    assert lib.fa_workspace_bytes(5, f16, capi.params(2, 1, 1, 2048, 64, 0.125, False)) == \
+        _split_bytes(2, 2 * 2048, 64)
+    assert lib.fa_workspace_bytes(5, bf16, capi.params(1, 2, 2, 8192, 128, 0.088, True)) == \
+        _split_bytes(2, 2 * 8192, 128)
+    for b, h, n, d, dt, causal in [(2, 8, 2048, 64, f16, False), (2, 8, 2048, 128, f16, False),
+                                   (2, 8, 2048, 128, f16, True), (1, 16, 8192, 128, bf16, True),
+                                   (1, 16, 512, 128, bf16, True), (1, 16, 1024, 128, bf16, True),
+                                   (8, 12, 1024, 64, f16, True)]:
+        assert lib.fa_workspace_bytes(5, dt, capi.params(b, h, h, n, d, 0.1, causal)) == 0
+    # Stages 3 and 4 never split; fp32 has no stage-5 kernel.
+    p = capi.params(2, 1, 1, 2048, 64, 0.125, False)
+    assert lib.fa_workspace_bytes(3, f16, p) == 0 and lib.fa_workspace_bytes(4, f16, p) == 0
+    assert lib.fa_workspace_bytes(5, capi.FA_DTYPE_F32, p) == 0
+    # FA_FORCE_SPLITS (test-only) forces S, capped at 16.
+    monkeypatch.setenv("FA_FORCE_SPLITS", "3")
+    assert lib.fa_workspace_bytes(5, f16, capi.params(1, 2, 2, 256, 64, 0.125, True)) == \
+        _split_bytes(3, 2 * 256, 64)
+    monkeypatch.setenv("FA_FORCE_SPLITS", "99")
+    assert lib.fa_workspace_bytes(5, bf16, capi.params(1, 1, 1, 128, 128, 0.1, False)) == \
+        _split_bytes(16, 128, 128)
+
+
 def test_impl_supports_registry():
     lib = capi.load()
     f32, f16, bf16 = capi.FA_DTYPE_F32, capi.FA_DTYPE_F16, capi.FA_DTYPE_BF16

@@ -1,0 +1,124 @@
+"""Split key walks of stage 5 (marker ``gpu``).
+
+With a workspace, stage 5 may cut every query tile's key walk into S parts of whole key tiles,
+one workgroup each. Each part writes its normalised fp32 O and its LSE to the workspace, and
+``fa_s5_combine`` merges them with the log-sum-exp rule (ref:include/fa/softmax_math.cuh:65-68).
+The library splits where its cost model says the GPU would otherwise sit idle (one GPU's share of
+a head-sharded problem); ``FA_FORCE_SPLITS`` forces S for these tests.
+
+* Forced S in {2, 3, 5} on full and causal problems, fp16 and bf16, D 64 and 128, with N an odd
+  multiple of 32 (partial tiles), against the fp64 oracle at the stated tolerance.
+* More parts than key tiles: the empty parts carry LSE = -inf and weigh nothing.
+* The shapes the model splits by itself: the C-ABI asks for a workspace, and the op
+  (``torch.ops.fused_attn.forward``, which allocates what ``fa_workspace_bytes`` asks for) and the
+  C-ABI without a workspace (the whole-walk kernel) both match the oracle.
+* A split launch (two kernels) captured into a HIP graph replays bit-identically.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import fused_attn
+from _checks import check_against_reference
+from fused_attn import capi
+
+pytestmark = pytest.mark.gpu
+
+
+def _require():
+    if not fused_attn.is_available():
+        pytest.fail("fused_attn._C is not built: the HIP path must be the one that runs")
+
+
+def _inputs(b, h, n, d, dtype, seed):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    return tuple(torch.randn(b, h, n, d, generator=g).to("cuda", dtype) for _ in range(3))
+
+
+def _split_run(q, k, v, causal, scale):
+    nbytes = capi.workspace_bytes(5, q, k, causal, scale)
+    assert nbytes > 0, "the split path needs a workspace"
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    o = torch.empty_like(q)
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device="cuda")
+    rc = capi.forward(5, q, k, v, o, lse, causal, scale, workspace=ws)
+    assert rc == capi.HIP_SUCCESS, capi.error_string(rc)
+    torch.cuda.synchronize()
+    return o, lse
+
+
+@pytest.mark.parametrize("splits", [2, 3, 5])
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("b,h,n,d", [(1, 2, 352, 64), (2, 3, 224, 128), (1, 1, 1024, 64)],
+                         ids=lambda x: str(x))
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_forced_splits_match_oracle(b, h, n, d, dtype, causal, splits, monkeypatch):
+    _require()
+    monkeypatch.setenv("FA_FORCE_SPLITS", str(splits))
+    q, k, v = _inputs(b, h, n, d, dtype, seed=splits + 10 * n)
+    o, lse = _split_run(q, k, v, causal, 1.0 / math.sqrt(d))
+    check_against_reference(o, q, k, v, causal, dtype, lse=lse)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_more_parts_than_key_tiles(dtype, monkeypatch):
+    """N = 96 at D = 128 is 2 key tiles of 64 (the first query tile's causal walk is 1): most of
+    the 7 parts are empty."""
+    _require()
+    monkeypatch.setenv("FA_FORCE_SPLITS", "7")
+    q, k, v = _inputs(2, 2, 96, 128, dtype, seed=5)
+    for causal in (False, True):
+        o, lse = _split_run(q, k, v, causal, 1.0 / math.sqrt(128))
+        check_against_reference(o, q, k, v, causal, dtype, lse=lse)
+
+
+@pytest.mark.parametrize("b,h,n,d,dtype,causal", [
+    (2, 1, 2048, 64, torch.float16, False),    # C64 over 8 GPUs by heads
+    (1, 2, 4096, 128, torch.bfloat16, True),   # a LONG-like share by heads (N halved)
+], ids=["C64-heads8", "long-heads"])
+def test_model_splits_share_shapes(b, h, n, d, dtype, causal, monkeypatch):
+    _require()
+    monkeypatch.delenv("FA_FORCE_SPLITS", raising=False)
+    q, k, v = _inputs(b, h, n, d, dtype, seed=21)
+    scale = 1.0 / math.sqrt(d)
+    assert capi.workspace_bytes(5, q, k, causal, scale) > 0, "the cost model should split here"
+    o_op = fused_attn.forward(q, k, v, is_causal=causal)  # the op allocates the workspace
+    o_whole = torch.empty_like(q)
+    lse_whole = torch.empty(b, h, n, dtype=torch.float32, device="cuda")
+    assert capi.forward(5, q, k, v, o_whole, lse_whole, causal, scale, workspace=None) == 0
+    torch.cuda.synchronize()
+    check_against_reference(o_op, q, k, v, causal, dtype)
+    check_against_reference(o_whole, q, k, v, causal, dtype, lse=lse_whole)
+
+
+def test_split_launch_in_graph(monkeypatch):
+    """Both kernels of a split launch replay from a graph, bit-identical to the eager launch."""
+    _require()
+    monkeypatch.setenv("FA_FORCE_SPLITS", "3")
+    q, k, v = _inputs(1, 4, 512, 128, torch.bfloat16, seed=8)
+    scale = 0.088
+    ws = torch.empty(capi.workspace_bytes(5, q, k, True, scale), dtype=torch.uint8, device="cuda")
+    o = torch.empty_like(q)
+    lse = torch.empty(1, 4, 512, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        assert capi.forward(5, q, k, v, o, lse, True, scale, stream=stream, workspace=ws) == 0
+    stream.synchronize()
+    o_ref, lse_ref = o.clone(), lse.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        capi.forward(5, q, k, v, o, lse, True, scale, stream=stream, workspace=ws)
+    for r in range(3):
+        o.zero_()
+        lse.zero_()
+        x = torch.randn(256, 256, device="cuda")
+        (x @ x).sum().item()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()
+        stream.synchronize()
+        assert torch.equal(o, o_ref) and torch.equal(lse, lse_ref), f"replay {r} differs"
