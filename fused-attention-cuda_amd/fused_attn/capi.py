@@ -161,16 +161,23 @@ def strides_of(t: torch.Tensor) -> FaStrides:
 
 def forward_strided(impl: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
                     lse: torch.Tensor, is_causal: bool, scale: float,
-                    stream: torch.cuda.Stream | None = None) -> int:
-    """``fa_forward_strided`` on torch views (their own strides); returns the hipError_t value."""
+                    stream: torch.cuda.Stream | None = None,
+                    workspace: torch.Tensor | None | str = "auto") -> int:
+    """``fa_forward_strided`` on torch views (their own strides); returns the hipError_t value.
+    ``workspace`` as for ``forward``."""
     b, h, n, d = q.shape
     p = params(b, h, k.shape[1], n, d, scale, is_causal)
     s = stream if stream is not None else torch.cuda.current_stream(q.device)
+    if isinstance(workspace, str):
+        nbytes = workspace_bytes(impl, q, k, is_causal, scale)
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
     qs, ks, vs, os_ = strides_of(q), strides_of(k), strides_of(v), strides_of(o)
     return load().fa_forward_strided(impl, DTYPE_CODES[q.dtype], q.data_ptr(), ctypes.byref(qs),
                                      k.data_ptr(), ctypes.byref(ks), v.data_ptr(),
                                      ctypes.byref(vs), o.data_ptr(), ctypes.byref(os_),
-                                     lse.data_ptr(), None, ctypes.byref(p), s.cuda_stream)
+                                     lse.data_ptr(),
+                                     None if workspace is None else workspace.data_ptr(),
+                                     ctypes.byref(p), s.cuda_stream)
 
 
 def decode_params(q: torch.Tensor, k: torch.Tensor, is_causal: bool, scale: float,

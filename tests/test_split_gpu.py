@@ -122,3 +122,27 @@ def test_split_launch_in_graph(monkeypatch):
             graph.replay()
         stream.synchronize()
         assert torch.equal(o, o_ref) and torch.equal(lse, lse_ref), f"replay {r} differs"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_split_strided_views(dtype, monkeypatch):
+    """fa_forward_strided with a split: q/k/v are head splits of [B, N, H, D] buffers and o a view
+    into a wider buffer. The combine writes exactly o's elements, and the result equals the split
+    launch on contiguous copies bit for bit (same arithmetic, other addresses)."""
+    _require()
+    monkeypatch.setenv("FA_FORCE_SPLITS", "3")
+    b, h, n, d = 2, 3, 224, 64
+    g = torch.Generator(device="cpu").manual_seed(17)
+    q, k, v = (torch.randn(b, n, h, d, generator=g).to("cuda", dtype).transpose(1, 2)
+               for _ in range(3))
+    big = torch.full((b, n, h + 1, d), 7.0, dtype=dtype, device="cuda")
+    o = big[:, :, 1:].transpose(1, 2)
+    lse = torch.empty(b, h, n, dtype=torch.float32, device="cuda")
+    scale = 1.0 / math.sqrt(d)
+    assert capi.forward_strided(5, q, k, v, o, lse, True, scale) == 0  # workspace "auto"
+    torch.cuda.synchronize()
+    assert torch.all(big[:, :, 0] == 7.0)
+    o_ref, lse_ref = _split_run(q.contiguous(), k.contiguous(), v.contiguous(), True, scale)
+    assert torch.equal(o, o_ref) and torch.equal(lse, lse_ref)
+    check_against_reference(o.contiguous(), q.contiguous(), k.contiguous(), v.contiguous(), True,
+                            dtype, lse=lse)
