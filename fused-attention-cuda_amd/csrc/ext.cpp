@@ -152,8 +152,9 @@ std::tuple<at::Tensor, at::Tensor> run_stage(const at::Tensor& q, const at::Tens
   const bool has_lse = stage >= kFirstLseStage;
   at::Tensor lse = has_lse ? at::empty({p.B, p.H, p.N}, q.options().dtype(at::kFloat))
                            : at::empty({0}, q.options().dtype(at::kFloat));
-  // Scratch for the materialising stages only (0 bytes for the fused ones); freed stream-ordered
-  // by the caching allocator after the asynchronous launch.
+  // Scratch for the materialising stages, and stage 5's optional workspace where it splits key
+  // walks (0 bytes otherwise); freed stream-ordered by the caching allocator after the
+  // asynchronous launch.
   const size_t ws_bytes = fa_workspace_bytes(impl, dtype, &p);
   at::Tensor workspace;
   void* ws_ptr = nullptr;
@@ -212,11 +213,17 @@ at::Tensor forward_strided_cuda(const at::Tensor& q, const at::Tensor& k, const 
   at::Tensor o = empty_in_layout_of(q);
   at::Tensor lse = at::empty({p.B, p.H, p.N}, q.options().dtype(at::kFloat));
   const fa_strides qs = strides_of(q), ks = strides_of(k), vs = strides_of(v), os = strides_of(o);
+  // Stage 5's optional workspace (split key walks), as in forward.
+  const size_t ws_bytes = fa_workspace_bytes(stage, dtype, &p);
+  at::Tensor workspace;
+  if (ws_bytes > 0) {
+    workspace = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+  }
   const hipStream_t stream =
       c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.device().index()).stream();
   const int err = fa_forward_strided(stage, dtype, q.data_ptr(), &qs, k.data_ptr(), &ks,
                                      v.data_ptr(), &vs, o.data_ptr(), &os, lse.data_ptr<float>(),
-                                     nullptr, &p, stream);
+                                     ws_bytes > 0 ? workspace.data_ptr() : nullptr, &p, stream);
   TORCH_CHECK(err == 0, "fused_attn: stage ", stage, " (", fa_impl_name(stage),
               ") failed: ", fa_error_string(err));
   return o;

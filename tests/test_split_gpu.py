@@ -146,3 +146,17 @@ def test_split_strided_views(dtype, monkeypatch):
     assert torch.equal(o, o_ref) and torch.equal(lse, lse_ref)
     check_against_reference(o.contiguous(), q.contiguous(), k.contiguous(), v.contiguous(), True,
                             dtype, lse=lse)
+
+
+def test_op_strided_splits(monkeypatch):
+    """torch.ops.fused_attn.forward_strided allocates the split workspace as forward does."""
+    _require()
+    monkeypatch.setenv("FA_FORCE_SPLITS", "2")
+    g = torch.Generator(device="cpu").manual_seed(23)
+    q, k, v = (torch.randn(1, 256, 4, 128, generator=g).to("cuda", torch.bfloat16).transpose(1, 2)
+               for _ in range(3))
+    o = fused_attn.forward_strided(q, k, v, is_causal=True)
+    o_ref = fused_attn.forward(q.contiguous(), k.contiguous(), v.contiguous(), is_causal=True)
+    assert torch.equal(o, o_ref)
+    check_against_reference(o_ref, q.contiguous(), k.contiguous(), v.contiguous(), True,
+                            torch.bfloat16)
