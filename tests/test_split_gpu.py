@@ -160,3 +160,17 @@ def test_op_strided_splits(monkeypatch):
     assert torch.equal(o, o_ref)
     check_against_reference(o_ref, q.contiguous(), k.contiguous(), v.contiguous(), True,
                             torch.bfloat16)
+
+
+@pytest.mark.parametrize("hkv", [1, 2])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_gqa_splits(hkv, dtype, monkeypatch):
+    """GQA / MQA with split walks: query head h reads kv head h // (H / Hkv) in every part."""
+    _require()
+    monkeypatch.setenv("FA_FORCE_SPLITS", "3")
+    g = torch.Generator(device="cpu").manual_seed(31 + hkv)
+    q = torch.randn(1, 4, 352, 128, generator=g).to("cuda", dtype)
+    k, v = (torch.randn(1, hkv, 352, 128, generator=g).to("cuda", dtype) for _ in range(2))
+    for causal in (False, True):
+        o, lse = _split_run(q, k, v, causal, 1.0 / math.sqrt(128))
+        check_against_reference(o, q, k, v, causal, dtype, lse=lse)
