@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
-"""Benchmark of the fused SDPA forward on one MI355X (the BASELINE.json metric).
+"""Benchmark of the fused SDPA forward on one MI355X (the reference's headline metric: forward
+time and TFLOP/s at B2 H8 N2048, D 64 / 128, fp16).
 
-Headline workload: C64 = B2 H8 N2048 D64, fp16 in / fp32 accumulate,
+Headline workload: C64 = B2 H8 N2048 D64 (ref:bench/bench_main.cu:241-243), fp16 in / fp32 accumulate,
 non-causal, through the stage-5 kernel (``fa_s5_tuned``, what ``torch.ops.fused_attn.forward``
 dispatches to for fp16). A *step* is one forward over one batch of synthetic inputs already
 resident in HBM. The kernel is launched through the C-ABI (``fa_forward`` of libfa_hip.so) on a
@@ -17,8 +18,8 @@ Printed: ONE JSON line with the contract fields, plus
 * ``cpu_baseline``: the reference's own fp64 CPU oracle (oracle/_ref, ``fa::ref::attention_rows``,
   kind "reference"; the C restatement, kind "port", when _ref is absent) timed on the host cores
   over the same workload, repeated for a bounded budget of CPU time;
-* ``configs``: the other BASELINE configurations measured the same way (C128, C128 causal, LONG
-  with its N sweep 512 / 1024 / 4096 / 8192, GPT attention shape), each with ms and TFLOP/s
+* ``configs``: the other benchmark configurations measured the same way (C128, C128 causal, the
+  long-context shape LONG with its N sweep 512 / 1024 / 4096 / 8192, the GPT-2 attention shape), each with ms and TFLOP/s
   (graph replay) and ``eager_ms``, plus one GPU's share of 8-GPU layouts (C64 and LONG split
   over heads, one ring step of LONG split over the sequence);
 * ``vendor_sdpa``: torch's ``scaled_dot_product_attention`` on the same inputs (fp16 configs);
@@ -46,14 +47,14 @@ sys.path.insert(0, str(ROOT / "fused-attention-cuda_amd"))
 
 METRIC = "fwd ms + TFLOP/s, B2 H8 N2048 D64/D128 fp16; % of MFMA fp16 peak"
 PEAK_TFLOPS = {"fp16": 2500.0, "bf16": 2500.0, "fp32": 157.3}  # MI355X dense MFMA
-# (name, B, H, N, D, dtype, causal, input std): BASELINE.json configs[1..4] (attention shapes).
+# (name, B, H, N, D, dtype, causal, input std): the attention shapes of the benchmark.
 WORKLOADS = {
     "C64": (2, 8, 2048, 64, "fp16", False, 1.0),
     "C128": (2, 8, 2048, 128, "fp16", False, 1.0),
     "C128_causal": (2, 8, 2048, 128, "fp16", True, 1.0),
     "LONG": (1, 16, 8192, 128, "bf16", True, 0.5),
     "GPT_attn": (8, 12, 1024, 64, "fp16", True, 1.0),
-    # The rest of BASELINE config 4's sweep (N in 512 / 1024 / 4096 beside LONG's 8192).
+    # The rest of LONG's N sweep (512 / 1024 / 4096 beside 8192).
     "LONG_N512": (1, 16, 512, 128, "bf16", True, 0.5),
     "LONG_N1024": (1, 16, 1024, 128, "bf16", True, 0.5),
     "LONG_N4096": (1, 16, 4096, 128, "bf16", True, 0.5),
@@ -363,7 +364,7 @@ def decode_line(torch):
 
 
 def gpt_block_line(torch):
-    """one GPT-2-small decoder block (768 wide, 12 heads of 64, T 1024, batch 8,
+    """The GPT-2-small block benchmark (ref:bench/gpt_block.py:53-158): one decoder block (768 wide, 12 heads of 64, T 1024, batch 8,
     fp16, causal, random init, random token ids through a wte/wpe embedding), tokens/s with the
     attention call swapped (fused strided op / fused op after .contiguous() copies / torch SDPA);
     warm timing as the reference's ref:bench/gpt_block.py:141-158."""
@@ -400,8 +401,10 @@ def main(argv=None) -> int:
                          "WRITE_SIZE scaling)")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU; multi-GPU runs are out of scope "
-              "(see the sharding note in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py: this build measures one GPU; multi-GPU runs are out of scope. Every "
+              "configuration shards over heads with no communication, and one GPU's share is "
+              "measured instead (configs C64_heads8, LONG_heads8, LONG_ring8). Run with --gpus 1.",
+              file=sys.stderr)
         return 2
 
     import torch

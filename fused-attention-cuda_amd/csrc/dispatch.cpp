@@ -305,9 +305,11 @@ VariantList s5_list(int dtype) {
 //   combine  = (2 S + 0.5) * rows * D * 4 bytes at 4 TB/s (the parts written, read back, and O)
 //              + 2 us for the second launch.
 // The S in 2..16 with the least time is taken when it saves at least 20 % over S = 1. On MI355X
-// this splits the shapes of one GPU's share of a head-sharded problem (C64's 2 heads of 16,
-// LONG's 2 of 16) and leaves every BASELINE configuration whole. FA_FORCE_SPLITS (test-only)
-// forces S; fa_workspace_bytes and fa_forward must see the same value.
+// this splits one GPU's share of a head-sharded problem (2 heads of B2 H8 N2048 D64, 2 of
+// B1 H16 N8192 D128 causal) and leaves whole the benchmark shapes that fill the GPU (B2 H8 N2048
+// at D 64 and 128, causal or not; B1 H16 at N 512-8192 causal; B8 H12 N1024 D64 causal).
+// FA_FORCE_SPLITS (test-only) forces S; fa_workspace_bytes and fa_forward must see the same
+// value.
 constexpr int kMaxSplits = 16;
 int s5_splits(const fa_params& p, int dtype) {
   if (const int f = env_positive_int("FA_FORCE_SPLITS")) return std::min(f, kMaxSplits);

@@ -1,7 +1,7 @@
 """GPT-2-small decoder block with a swappable attention call, and its tokens/s measurement.
 
 This is the end-to-end consumer of the op, restating the reference's nanoGPT block check
-(ref:bench/gpt_block.py:53-158) for BASELINE config 5:
+(ref:bench/gpt_block.py:53-158), the reference's GPT-2-small block benchmark:
 - token + position embedding (wte 50257 x 768, wpe 1024 x 768);
 - LayerNorm -> causal self-attention (12 heads of 64) -> residual;
 - LayerNorm -> MLP (768 -> 3072 -> 768, GELU) -> residual;
@@ -125,7 +125,7 @@ def build(kind: str, n_embd: int = 768, n_head: int = 12, dtype=torch.float16, s
 
 
 def token_ids(batch: int = 8, seq: int = 1024, seed: int = 0, device: str = "cuda"):
-    """Random token ids in [0, 50257)."""
+    """Random token ids in [0, 50257) (the GPT-2 vocabulary)."""
     gen = torch.Generator(device="cpu").manual_seed(seed)
     return torch.randint(0, VOCAB, (batch, seq), generator=gen).to(device)
 

@@ -84,7 +84,8 @@ def main() -> int:
         print("oracle/_ref/libfa_ref.so missing: run `make -C oracle ref` first", file=sys.stderr)
         return 2
     closed_form()
-    # B1 H2 N128 D64 fp32, scale 1/sqrt(D); tiled outputs pin the recurrence.
+    # The reference's CPU-runnable case: B1 H2 N128 D64 fp32, scale 1/sqrt(D); tiled outputs pin
+    # the recurrence.
     case("cpu_b1h2n128d64_f32", 1, 2, 128, 64, seed=0, tiles=((32, 16, 0), (32, 16, 1)))
     # GQA head mapping at D=128 with a non-default scale and partial tiles (N=96).
     case("gqa_b1h2kv1n96d128_f32", 1, 2, 96, 128, hkv=1, seed=3, scale=0.05, tiles=((64, 64, 1),))

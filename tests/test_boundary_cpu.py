@@ -76,7 +76,7 @@ def test_stage5_split_workspace(monkeypatch):
     """Stage 5 asks for a workspace (fp32 partial O [S, B, H, N, D] + LSE [S, B, H, N]) only where
     its cost model splits the key walks. Without a device the model assumes 256 CUs (MI355X):
     one GPU's share of C64 over 8 GPUs (B2 H1) and of LONG (B1 H2 N8192 causal) split in two,
-    the BASELINE configurations and the GPT-2 attention shape do not."""
+    the whole benchmark shapes and the GPT-2 attention shape do not."""
     monkeypatch.delenv("FA_FORCE_SPLITS", raising=False)
     lib = capi.load()
     f16, bf16 = capi.FA_DTYPE_F16, capi.FA_DTYPE_BF16

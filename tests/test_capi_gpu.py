@@ -1,8 +1,8 @@
 """GPU parity through the C-ABI (marker ``gpu``): ``fa_forward`` of libfa_hip.so called with ctypes
 on device buffers, with no torch op in between.
 
-* Golden vectors written by the reference's own fp64 oracle (tests/golden/) -- the BASELINE CPU
-  config (B1 H2 N128 D64 fp32), a GQA/D128/partial-tile case and rounded fp16/bf16 inputs -- on
+* Golden vectors written by the reference's own fp64 oracle (tests/golden/) -- the reference's
+  CPU-runnable case (B1 H2 N128 D64 fp32), a GQA/D128/partial-tile case and rounded fp16/bf16 inputs -- on
   every stage that takes the dtype, to the stated tolerance.
 * Status codes of the boundary on a real device (ref:src/dispatch.cu:140-161,
   ref:src/stage5_tuned.cu:983-1026): unsupported stage -> hipErrorNotSupported; misaligned

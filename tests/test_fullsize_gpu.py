@@ -1,4 +1,4 @@
-"""Parity at the BASELINE sizes (marker ``gpu``).
+"""Parity at the benchmark sizes (marker ``gpu``).
 
 The fp64 oracle cannot afford whole B2 H8 N2048 or B1 H16 N8192 problems in a test, so each config
 is checked three ways:
@@ -27,7 +27,8 @@ from oracle.oracle import math_reference_rows
 
 pytestmark = pytest.mark.gpu
 
-# (name, B, H, N, D, dtype, causal, input std) -- BASELINE.json configs 2-5 and the LONG N sweep.
+# (name, B, H, N, D, dtype, causal, input std): C64 / C128 (ref:bench/bench_main.cu:241-243),
+# C128 causal, the long-context shape LONG and its N sweep, the GPT-2 attention shape.
 CONFIGS = [
     ("C64", 2, 8, 2048, 64, torch.float16, False, 1.0),
     ("C128", 2, 8, 2048, 128, torch.float16, False, 1.0),

@@ -1,4 +1,4 @@
-"""The GPT-2-small block harness runs its attention through the fused op
+"""The GPT-2-small block harness (ref:bench/gpt_block.py:53-158) runs its attention through the fused op
 (marker ``gpu``): the strided call inside the block equals the dense call bitwise, the block's
 attention matches an fp32 torch computation of the same attention, and the timing helper runs."""
 

@@ -1,7 +1,7 @@
 """HIP graph capture of the forward and decode paths (marker ``gpu``).
 
-INTEGRATION.md states that callers under HIP graph capture can use ``fa_forward`` directly (the
-library allocates nothing and records no memset). These tests capture launches into a
+Callers under HIP graph capture can use ``fa_forward`` directly: the library allocates nothing
+and records no memset. These tests capture launches into a
 ``torch.cuda.CUDAGraph``, replay the graph several times with unrelated eager work and
 synchronisations in between, and compare every replay bitwise with the eager launches (the
 kernels are deterministic). The outputs are cleared before each replay, so a replay that did not
