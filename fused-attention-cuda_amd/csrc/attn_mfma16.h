@@ -678,13 +678,16 @@ struct Fa16 {
       using P1 = std::integral_constant<int, 1>;
       // Tiles [0, n_full) are full for every wave and carry no diagonal (workgroup-uniform): key
       // tile t is complete below the workgroup's first row (causal) or below N. When every tile of
-      // [t0, n_tiles) is full all of them take the steady step; otherwise steady step t also needs
-      // tile t+1 full and K(t+2) a whole tile inside the tensor (t + 3 <= N / BC), so that its
-      // loads need no clamp. Steady steps are t in [t0, n_steady).
+      // [t0, n_tiles) is full all of them take the steady step. Otherwise steady step t needs tile
+      // t itself full and diagonal-free, tile t+1 inside the walk, and V(t+1) and K(t+2) whole
+      // tiles inside the tensor (t + 3 <= N / BC), so that its loads need no clamp. Tile t+1 may
+      // carry the causal diagonal: the steady step only computes its scores, unmasked, and the
+      // partial step that exponentiates them applies the mask and the per-wave block counts.
+      // Steady steps are t in [t0, n_steady).
       const int n_full = (a.causal ? i0 : N) / BC;
       const int n_steady = n_full >= n_tiles
                                ? n_tiles
-                               : max(t0, min(min(n_tiles, n_full) - 1, N / BC - 2));
+                               : max(t0, min(min(n_tiles - 1, n_full), N / BC - 2));
       // Unrolled by two so the S(t) / S(t+1) register sets swap roles without copies; the steady
       // loop and the tail loop get independent register assignments.
       int t = t0;
