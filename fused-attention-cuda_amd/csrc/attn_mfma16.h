@@ -79,6 +79,12 @@ constexpr int kNumXcd = 8;
 constexpr float kLn2 = 0.69314718055994531f;
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// floor(n / d) for 0 <= n < 2^31 from the launch's precomputed FastDiv (two scalar instructions
+// for a uniform n).
+__device__ __forceinline__ int fdiv(int n, const FastDiv& f) {
+  return f.d == 1 ? n : static_cast<int>(__umulhi(static_cast<uint32_t>(n), f.m) >> f.s);
+}
 __device__ __forceinline__ float log2_hw(float x) { return __builtin_amdgcn_logf(x); }
 
 // 8 fp32 probabilities -> one 16-byte MFMA operand (round to nearest even).
@@ -551,14 +557,14 @@ struct Fa16 {
     // (readfirstlane: uniform integer divisions run on the vector unit, and their results would
     // otherwise occupy vector registers for the whole kernel.)
     const int S = a.n_splits;
-    const int item = __builtin_amdgcn_readfirstlane(S > 1 ? logical / S : logical);
+    const int item = __builtin_amdgcn_readfirstlane(fdiv(logical, a.fd_splits));
     const int part = logical - item * S;
-    const int bh = item / a.n_qtiles;
+    const int bh = fdiv(item, a.fd_qtiles);
     int qt = item - bh * a.n_qtiles;
     if (a.causal) qt = a.n_qtiles - 1 - qt;  // longest key ranges first
-    const int b = bh / a.H;
+    const int b = fdiv(bh, a.fd_h);
     const int h = bh - b * a.H;
-    const int hk = h / (a.H / a.Hkv);
+    const int hk = fdiv(h, a.fd_group);
     const int N = a.N;
 
     const T* qb = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
@@ -573,8 +579,8 @@ struct Fa16 {
     // walks key tiles [t0, n_tiles): the whole walk, or its part of a split walk.
     const int kv_end = a.causal ? min(N, i0 + kBr) : N;
     const int n_walk = (kv_end + BC - 1) / BC;
-    const int t0 = __builtin_amdgcn_readfirstlane(part * n_walk / S);
-    const int n_tiles = __builtin_amdgcn_readfirstlane((part + 1) * n_walk / S);
+    const int t0 = __builtin_amdgcn_readfirstlane(fdiv(part * n_walk, a.fd_splits));
+    const int n_tiles = __builtin_amdgcn_readfirstlane(fdiv((part + 1) * n_walk, a.fd_splits));
     const int wave_end = wave_valid ? (a.causal ? min(N, r0 + 32) : N) : 0;
     const int kbase = ks * BCW;  // this wave's keys inside every tile
     const float c = a.c;
@@ -890,6 +896,7 @@ int launch(const KArgs& in, hipStream_t stream) {
   using A = Fa16<T, D, RG, KS, BCW, STAGE == 5>;
   KArgs a = in;
   a.n_qtiles = (a.N + A::kBr - 1) / A::kBr;
+  a.fd_qtiles = make_fastdiv(static_cast<uint32_t>(a.n_qtiles));
   if (a.n_splits < 1 || (a.n_splits > 1 && (STAGE != 5 || a.o_part == nullptr ||
                                             a.lse_part == nullptr))) {
     return static_cast<int>(hipErrorInvalidValue);

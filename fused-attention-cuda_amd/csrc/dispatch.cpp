@@ -200,6 +200,10 @@ KArgs make_args(const void* q, const void* k, const void* v, void* o, float* lse
   a.n_splits = 1;
   a.o_part = nullptr;
   a.lse_part = nullptr;
+  a.fd_h = make_fastdiv(static_cast<uint32_t>(p.H));
+  a.fd_group = make_fastdiv(static_cast<uint32_t>(p.H / p.Hkv));
+  a.fd_splits = make_fastdiv(1);
+  // fd_qtiles: set by the launcher with n_qtiles.
   return a;
 }
 
@@ -393,6 +397,7 @@ int forward(int dtype, const void* q, const void* k, const void* v, void* o, flo
   const LaunchFn combine = dtype == FA_DTYPE_F16 ? combine_s5_f16(p.D) : combine_s5_bf16(p.D);
   if (combine == nullptr) return static_cast<int>(hipErrorNotSupported);
   a.n_splits = splits;
+  a.fd_splits = make_fastdiv(static_cast<uint32_t>(splits));
   a.o_part = static_cast<float*>(workspace);
   a.lse_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + s5_opart_bytes(p, splits));
   const int lrc = launch_selected("stage5", list, br, bc, a, p.D, stream);

@@ -10,6 +10,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 
@@ -21,6 +22,29 @@ struct Overrides {
   int block_m = 0;  // forced BR (query rows per workgroup); 0 = default
   int block_n = 0;  // forced BC (keys per K/V tile); 0 = default
 };
+
+// Division by a launch constant d >= 1 without a divide instruction (Granlund-Montgomery,
+// "round-up" variant): with l = ceil(log2 d) and p = 31 + l, m = ceil(2^p / d) fits 32 bits and
+// floor(n / d) = floor(n * m / 2^p) for every n < 2^31, because n * (m - 2^p / d) / 2^p < 1 / d.
+// d = 1 is special-cased (it would need p = 31 < 32). The host fills the struct once per launch;
+// the kernel's uniform quotients are then two scalar instructions instead of a float-reciprocal
+// sequence on the vector unit.
+struct FastDiv {
+  uint32_t d = 1;
+  uint32_t m = 0;
+  uint32_t s = 0;  // p - 32
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  f.d = d < 1 ? 1 : d;
+  if (f.d == 1) return f;
+  uint32_t l = 0;
+  while ((1ull << l) < f.d) ++l;
+  const unsigned long long p2 = 1ull << (31 + l);
+  f.m = static_cast<uint32_t>((p2 + f.d - 1) / f.d);
+  f.s = l - 1;
+  return f;
+}
 
 // Arguments of every kernel entry point (one struct in the kernarg segment).
 struct KArgs {
@@ -49,6 +73,8 @@ struct KArgs {
   int n_splits;
   float* o_part;
   float* lse_part;
+  // Divisors of the grid decode (see FastDiv): n_qtiles, H, H / Hkv and n_splits.
+  FastDiv fd_qtiles, fd_h, fd_group, fd_splits;
 };
 
 // Arguments of the split-KV decode kernels (attn_decode.h). q, o: [B, H, Nq, D]; k, v:
