@@ -623,18 +623,23 @@ struct Fa16 {
       // run, then applies P(t) to V(t). K is therefore staged one tile ahead of V: with u = t - t0,
       // iteration t reads K buffer (u+1)%2 and V buffer u%2 and refills K buffer u%2 with K(t+2)
       // and V buffer (u+1)%2 with V(t+1).
-      // K(t0), V(t0) and K(t0+1) in flight together (one memory round trip for the prologue).
+      // Prologue: wait only for Q and K(t0), which QK(t0) reads; V(t0) and K(t0+1) are issued
+      // after that wait (inline-asm DMA, which the compiler does not make QK's LDS reads wait
+      // for) and land while QK(t0) runs. The full wait before the second barrier publishes them.
       dma_tile<false>(kbuf0, kg, dk, t0 * BC, N, ksn, wave);
-      dma_tile<true>(vbuf0, vg, dv, t0 * BC, N, vsn, wave);
-      if (t0 + 1 < n_tiles) dma_tile<false>(kbuf0 + kKElems, kg, dk, (t0 + 1) * BC, N, ksn, wave);
       wait_dma();
       __syncthreads();
+      dma_tile_asm<true>(vbuf0, vg, dv, t0 * BC, N, vsn, wave);
+      if (t0 + 1 < n_tiles) {
+        dma_tile_asm<false>(kbuf0 + kKElems, kg, dk, (t0 + 1) * BC, N, ksn, wave);
+      }
       f32x16 sa[kKB], sb[kKB];
       {
         const int nv0 = nvalid_of(t0);
         if (nv0 > 0) qk<false>(sa, ws, kwave(0), nv0, kl);
       }
-      __syncthreads();  // K buffer 0 is refilled in iteration 0
+      wait_dma();
+      __syncthreads();  // V(t0), K(t0+1) visible; K buffer 0 is refilled in iteration 0
       // One pipeline step. `full` (a compile-time tag) selects the steady-state body: tiles t and
       // t+1 are full for every wave of the workgroup and carry no causal diagonal, so the body has
       // no per-block branches and the VALU softmax of S(t) interleaves with the MFMAs of S(t+1).
