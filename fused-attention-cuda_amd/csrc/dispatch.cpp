@@ -281,10 +281,25 @@ constexpr int kDefaultBcF32 = 32;
 // shared barrier) overlap one workgroup's fixed cost with another's steps. Measured: the GPT-2
 // attention shape (B8 H12 N1024 D64 fp16 causal, 4.5 tiles on average) 43.1 -> 37.3 us, while
 // C64 (16 tiles) stays faster at BR 128 (29.3 against 30.6 us).
+// A short key walk: fewer than 8 default key tiles per 128-row workgroup on average (causal:
+// about half of N / BC).
+bool short_walk_s5(const fa_params& p) {
+  const long long bc = default_bc_mfma(p.D);
+  const long long tiles = (p.N + bc - 1) / bc;
+  return (p.causal ? tiles + 1 : 2 * tiles) < 16;  // twice the average
+}
+
+// Stage-5 key-tile width when FA_FORCE_BC is unset: the default, except at D = 64 for short
+// walks. There BC 64 (32 keys per wave, about 150 VGPRs) lets three 4-wave workgroups share a
+// CU instead of two, hiding more of their fixed cost. Measured on the GPT-2 attention shape
+// (B8 H12 N1024 D64 fp16 causal, BR 64): 32.5 us against 37.1 us at BC 128.
+int auto_bc_s5(const fa_params& p) {
+  return (p.D == 64 && short_walk_s5(p)) ? 64 : default_bc_mfma(p.D);
+}
+
 int auto_br_s5(VariantList list, const fa_params& p, int bc) {
   const long long cus = current_device_cus();
-  const long long tiles = (p.N + bc - 1) / bc;
-  const bool short_walk = (p.causal ? tiles + 1 : 2 * tiles) < 16;  // twice the average
+  const bool short_walk = short_walk_s5(p);
   for (const int br : {128, 64}) {
     if (find_variant(list, p.D, br, bc) == nullptr) continue;
     if (br == 128 && short_walk && find_variant(list, p.D, 64, bc) != nullptr) continue;
@@ -318,7 +333,7 @@ constexpr int kMaxSplits = 16;
 int s5_splits(const fa_params& p, int dtype) {
   if (const int f = env_positive_int("FA_FORCE_SPLITS")) return std::min(f, kMaxSplits);
   if (p.B < 1 || p.H < 1 || p.N < 1) return 1;
-  const int bc = default_bc_mfma(p.D);
+  const int bc = auto_bc_s5(p);
   const int br = auto_br_s5(s5_list(dtype), p, bc);
   const double cus = static_cast<double>(current_device_cus());
   const long long n_qt = (p.N + br - 1) / br;
@@ -382,7 +397,7 @@ int forward(int dtype, const void* q, const void* k, const void* v, void* o, flo
   if (!supports(dtype, p.D, arch)) return static_cast<int>(hipErrorNotSupported);
   const int rc = common_stage_checks("stage5", q, k, v, o, lse, p);
   if (rc != 0) return rc;
-  const int bc = dbg.block_n != 0 ? dbg.block_n : default_bc_mfma(p.D);
+  const int bc = dbg.block_n != 0 ? dbg.block_n : auto_bc_s5(p);
   KArgs a = make_args(q, k, v, o, lse, p, st);
   const VariantList list = s5_list(dtype);
   const int br = dbg.block_m != 0 ? dbg.block_m : auto_br_s5(list, p, bc);

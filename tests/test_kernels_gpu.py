@@ -75,11 +75,11 @@ def test_matches_fp64_reference(stage, dtype, causal, gpu_shape, make_qkv):
 
 
 # Stage 5 runs every key tile through its steady step when all tiles are full (non-causal, N a
-# multiple of the default BC: 128 at D = 64, 64 at D = 128); the last two steps then load clamped
-# tiles into buffers nobody reads again. These lengths give 1 to 5 full tiles (odd and even
-# counts, so the unrolled-by-two loop ends on either parity) plus one ragged length.
-@pytest.mark.parametrize("n,d", [(128, 64), (384, 64), (640, 64), (64, 128), (192, 128),
-                                 (320, 128), (160, 128)],
+# multiple of BC); the last two steps then load clamped tiles into buffers nobody reads again.
+# These short problems run BC = 64 at both head dims, so the lengths give 1 to 10 full tiles (odd
+# and even counts, so the unrolled-by-two loop ends on either parity) plus one ragged length.
+@pytest.mark.parametrize("n,d", [(128, 64), (192, 64), (320, 64), (640, 64), (64, 128),
+                                 (192, 128), (320, 128), (160, 128)],
                          ids=lambda x: str(x))
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=_pair_id)
 def test_stage5_full_tile_counts(n, d, dtype, make_qkv):
