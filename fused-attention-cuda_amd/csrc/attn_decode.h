@@ -6,15 +6,16 @@
 // (ref:docs/RESEARCH.md:151-156): O = sum_s e^(L_s - L*) O_s / sum_s e^(L_s - L*), L* = max_s L_s.
 //
 // Included by attn_f16.hip and attn_bf16.hip. Kernel entry points:
-//   fa_decode_split<T, D>    one workgroup per (split, kv head, batch); 4 waves
-//   fa_decode_combine<T, D>  one wave per (batch, head, query token)
+//   fa_decode_split<T, D, RG>  one workgroup per (split, kv head, batch); 4 * RG waves
+//   fa_decode_combine<T, D>    one wave per (batch, head, query token)
 //
 // Work decomposition. The G = H / Hkv query heads of one kv head, times the Nq query tokens, are
 // R = G * Nq rows that read the same keys; in q ([B, H, Nq, D]) they are contiguous (head-major,
-// then token), so they form one 32-row MFMA tile (R <= 32 is required; rows past R are zero).
-// Keys stream through LDS in tiles of 128 (LDS-DMA, two buffers, the next tile in flight while
-// the current one is used); wave w takes keys [32 w, 32 w + 32) of every tile, and the four
-// partial (m, l, O) are merged through LDS at the end (the stage-5 machinery with RG = 1, KS = 4).
+// then token), so they form RG = 1 or 2 32-row MFMA tiles (R <= 64 is required; rows past R are
+// zero). Keys stream through LDS in tiles of 128 (LDS-DMA, two buffers, the next tile in flight
+// while the current one is used), shared by the row groups; wave w serves row group w % RG and
+// takes keys [32 k, 32 k + 32), k = w / RG, of every tile, and each row group's four partial
+// (m, l, O) are merged through LDS at the end (the stage-5 machinery with KS = 4).
 // Masking is per lane: row r is query token i = r % Nq, which sees keys j <= Nkv - Nq + i when
 // causal (bottom-right: the new tokens are the last Nq positions) and j <= Nkv - 1 otherwise.
 // Split boundaries are multiples of 128 keys, so only the last split has a ragged end.
@@ -45,9 +46,10 @@ __device__ __forceinline__ void dec_dma16(const void* src, uint32_t lds) {
                : "memory");
 }
 
-template <typename T, int D>
+// RG row groups of 32 query rows (R <= 32 * RG) x 4 key-split waves of 32 keys, 2 buffers.
+template <typename T, int D, int RG>
 struct Dec16 {
-  using F = Fa16<T, D, 1, 4, 32, true>;  // 32 rows, 4 key-split waves of 32 keys, 2 buffers
+  using F = Fa16<T, D, RG, 4, 32, true>;
   static constexpr int BC = F::BC;        // 128 keys per tile
   static constexpr int kWaves = F::kWaves;
   static constexpr int kThreads = F::kThreads;
@@ -74,6 +76,8 @@ struct Dec16 {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rg = wave % RG;  // row group: query rows 32 rg .. 32 rg + 31 of the kv head's R
+    const int ksp = wave / RG;  // key split: keys 32 ksp .. 32 ksp + 31 of every tile
     const int g = lane >> 5;
     const int s = blockIdx.x % a.S;
     const int bh = blockIdx.x / a.S;
@@ -82,7 +86,7 @@ struct Dec16 {
     const int k_begin = s * a.chunk;
     const int k_end = min(a.Nkv, k_begin + a.chunk);
     const int nk = k_end - k_begin;  // >= 1: the launcher only makes non-empty splits
-    const int row = lane & 31;
+    const int row = 32 * rg + (lane & 31);
     const bool row_valid = row < a.R;
     const int q0 = (b * a.H + hkv * a.G) * a.Nq;  // first query row of the group in q / o
     const float c = a.c;
@@ -109,7 +113,7 @@ struct Dec16 {
                   static_cast<size_t>(k_begin) * D;
     T* const kbuf0 = lds;
     T* const vbuf0 = lds + 2 * F::kKElems;
-    const int kbase = wave * 32;  // this wave's keys inside every tile
+    const int kbase = ksp * 32;  // this wave's keys inside every tile
     const typename F::KLane kl = F::k_lane(lane);
     const typename F::VLane vl = F::v_lane(lane);
     const typename F::Dma dk = F::template dma_lane<false>(wave, lane, D);
@@ -153,10 +157,11 @@ struct Dec16 {
       __syncthreads();
     }
 
-    // Merge the four waves' partial states of the rows (LDS is free after the last barrier).
+    // Merge the four key splits' partial states of each row group (LDS is free after the last
+    // barrier).
     float* mg = reinterpret_cast<float*>(lds_raw);
-    if (wave > 0) {
-      float* dst = mg + (wave - 1) * F::kMergeFloats;
+    if (ksp > 0) {
+      float* dst = mg + ((ksp - 1) * RG + rg) * F::kMergeFloats;
 #pragma unroll
       for (int db = 0; db < kDB; ++db) {
 #pragma unroll
@@ -166,10 +171,10 @@ struct Dec16 {
       dst[(kDB * 16 + 1) * 64 + lane] = ws.l;
     }
     __syncthreads();
-    if (wave > 0) return;
+    if (ksp > 0) return;
 #pragma unroll
-    for (int sp = 1; sp < kWaves; ++sp) {
-      const float* src = mg + (sp - 1) * F::kMergeFloats;
+    for (int sp = 1; sp < 4; ++sp) {
+      const float* src = mg + ((sp - 1) * RG + rg) * F::kMergeFloats;
       const float m1 = src[kDB * 16 * 64 + lane];
       const float l1 = src[(kDB * 16 + 1) * 64 + lane];
       const float m_new = fmaxf(ws.m, m1);
@@ -228,9 +233,9 @@ struct Dec16 {
   }
 };
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) void fa_decode_split(DecArgs a) {
-  Dec16<T, D>::run(a);
+template <typename T, int D, int RG>
+__global__ __launch_bounds__(256 * RG) void fa_decode_split(DecArgs a) {
+  Dec16<T, D, RG>::run(a);
 }
 
 // One wave per output row (b, h, i): the LSE-weighted sum of the S partial rows. Lane l owns
@@ -310,9 +315,17 @@ __global__ __launch_bounds__(256) void fa_decode_combine(DecArgs a) {
 template <typename T, int D>
 int launch_decode(const DecArgs& a, hipStream_t stream) {
   const long long grid = static_cast<long long>(a.S) * a.B * a.Hkv;
-  if (grid <= 0 || grid > 0x7fffffffLL) return static_cast<int>(hipErrorInvalidValue);
-  hipLaunchKernelGGL((fa_decode_split<T, D>), dim3(static_cast<unsigned>(grid)),
-                     dim3(Dec16<T, D>::kThreads), 0, stream, a);
+  if (grid <= 0 || grid > 0x7fffffffLL || a.R < 1 || a.R > 64) {
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  // One 32-row group for R <= 32; two (8 waves, the same K/V tiles) up to 64 rows.
+  if (a.R <= 32) {
+    hipLaunchKernelGGL((fa_decode_split<T, D, 1>), dim3(static_cast<unsigned>(grid)),
+                       dim3(Dec16<T, D, 1>::kThreads), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((fa_decode_split<T, D, 2>), dim3(static_cast<unsigned>(grid)),
+                       dim3(Dec16<T, D, 2>::kThreads), 0, stream, a);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.S == 1) return static_cast<int>(e);
   const long long rows = static_cast<long long>(a.B) * a.H * a.Nq;

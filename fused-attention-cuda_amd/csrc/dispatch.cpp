@@ -566,7 +566,7 @@ int fa_decode(int dtype, const void* q, const void* k, const void* v, void* o, f
                           : dtype == FA_DTYPE_F16 ? fa::decode_f16(p->D)
                           : dtype == FA_DTYPE_BF16 ? fa::decode_bf16(p->D)
                                                    : nullptr;
-  if (fn == nullptr || static_cast<long long>(G) * p->Nq > 32) {
+  if (fn == nullptr || static_cast<long long>(G) * p->Nq > 64) {
     if (fa::verbose()) {
       std::fprintf(stderr, "fa_decode: not supported: dtype %s, D %d, (H/Hkv)*Nq %lld, gfx%d\n",
                    fa_dtype_name(dtype), p->D, static_cast<long long>(G) * p->Nq, arch);

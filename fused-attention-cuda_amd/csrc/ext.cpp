@@ -299,7 +299,7 @@ std::tuple<at::Tensor, at::Tensor> decode_cuda(const at::Tensor& q, const at::Te
   TORCH_CHECK(err != static_cast<int>(hipErrorNotSupported),
               "fused_attn: decode is not implemented for ", fa_dtype_name(dtype), " D=", p.D,
               " with (H/Hkv)*Nq=", static_cast<int64_t>(p.H / p.Hkv) * p.Nq,
-              " (supported: fp16/bf16, D 64 or 128, (H/Hkv)*Nq <= 32, gfx950)");
+              " (supported: fp16/bf16, D 64 or 128, (H/Hkv)*Nq <= 64, gfx950)");
   TORCH_CHECK(err == 0, "fused_attn: decode failed: ", fa_error_string(err));
   return {o, lse};
 }

@@ -111,7 +111,7 @@ def decode(q: Tensor, k: Tensor, v: Tensor, is_causal: bool = False, scale: floa
     [B, Hkv, Nkv, D] -> (o [B, H, Nq, D], lse [B, H, Nq]). With ``is_causal`` token i sees keys
     j <= Nkv - Nq + i (bottom-right alignment). ``num_splits`` = 0 lets the library choose how
     many pieces of the key range run in parallel; the pieces are combined with LSE weights.
-    fp16/bf16, D 64 or 128, (H / Hkv) * Nq <= 32."""
+    fp16/bf16, D 64 or 128, (H / Hkv) * Nq <= 64."""
     _require_ext()
     return torch.ops.fused_attn.decode(q, k, v, bool(is_causal), _resolve_scale(q, scale),
                                        int(num_splits))

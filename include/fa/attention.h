@@ -137,8 +137,8 @@ FA_API const char* fa_error_string(int status);
  * With `causal` the new tokens are the last Nq positions (bottom-right alignment): token i sees
  * keys j <= Nkv - Nq + i; without it every token sees all Nkv keys.
  * Contract: dtype fp16 or bf16, D in {64, 128}, Nq >= 1, Nkv >= 1 (any length), H % Hkv == 0,
- * (H / Hkv) * Nq <= 32 (the query rows of one kv head fill one 32-row tile), finite scale > 0,
- * 16-byte aligned q/k/v/o. */
+ * (H / Hkv) * Nq <= 64 (the query rows of one kv head fill one or two 32-row tiles), finite
+ * scale > 0, 16-byte aligned q/k/v/o. */
 typedef struct fa_decode_params {
   int B;          /* batch */
   int H;          /* query heads */

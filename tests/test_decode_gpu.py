@@ -53,6 +53,9 @@ CASES = [
     (1, 2, 2, 1, 5, 64, False, 0),       # cache shorter than one 32-key block
     (3, 4, 4, 2, 129, 128, True, 0),     # one key past a tile
     (1, 4, 4, 8, 2048, 64, False, 1),    # a single split
+    (2, 16, 2, 6, 900, 128, True, 0),    # R = 48: two row groups, the second half full, ragged
+    (1, 64, 8, 8, 3000, 128, True, 0),   # R = 64: GQA 8:1 with 8 new tokens (speculative)
+    (1, 32, 1, 2, 513, 64, False, 2),    # R = 64 at D = 64 (MQA-like), 2 splits
 ]
 
 
@@ -126,16 +129,16 @@ def test_capi_decode_errors():
     q32, k32, v32 = (t.float() for t in (q, k, v))
     rc = capi.decode(q32, k32, v32, q32.clone(), lse, False, 0.125)
     assert rc == capi.HIP_ERROR_NOT_SUPPORTED
-    # more than 32 query rows per kv head
-    qb, kb, vb = make(1, 8, 1, 5, 256, 64, torch.float16, seed=10)
-    rc = capi.decode(qb, kb, vb, torch.empty_like(qb), torch.empty(1, 8, 5, device="cuda"), False,
+    # more than 64 query rows per kv head
+    qb, kb, vb = make(1, 8, 1, 9, 256, 64, torch.float16, seed=10)
+    rc = capi.decode(qb, kb, vb, torch.empty_like(qb), torch.empty(1, 8, 9, device="cuda"), False,
                      0.125)
     assert rc == capi.HIP_ERROR_NOT_SUPPORTED
 
 
 def test_op_error_messages_and_opcheck():
     require_ext()
-    q, k, v = make(1, 8, 1, 5, 256, 64, torch.float16, seed=11)
+    q, k, v = make(1, 8, 1, 9, 256, 64, torch.float16, seed=11)
     with pytest.raises(RuntimeError, match="not implemented"):
         fused_attn.decode(q, k, v)
     q, k, v = make(1, 6, 4, 1, 64, 64, torch.float16, seed=12)
