@@ -297,8 +297,8 @@ int auto_bc_s5(const fa_params& p) {
   return (p.D == 64 && short_walk_s5(p)) ? 64 : default_bc_mfma(p.D);
 }
 
-int auto_br_s5(VariantList list, const fa_params& p, int bc) {
-  const long long cus = current_device_cus();
+// `cus`: the compute units to fill (the current device's for a launch).
+int auto_br_s5(VariantList list, const fa_params& p, int bc, long long cus) {
   const bool short_walk = short_walk_s5(p);
   for (const int br : {128, 64}) {
     if (find_variant(list, p.D, br, bc) == nullptr) continue;
@@ -323,19 +323,22 @@ VariantList s5_list(int dtype) {
 //              + (S > 1 ? combine : 0)
 //   combine  = (2 S + 0.5) * rows * D * 4 bytes at 4 TB/s (the parts written, read back, and O)
 //              + 2 us for the second launch.
-// The S in 2..16 with the least time is taken when it saves at least 20 % over S = 1. On MI355X
+// The S in 2..16 with the least time is taken when it saves at least 20 % over S = 1. The model
+// assumes MI355X's 256 CUs whatever the current device: S sets the workspace size, so it must
+// depend on the problem only (a workspace sized on one device stays valid on another). On MI355X
 // this splits one GPU's share of a head-sharded problem (2 heads of B2 H8 N2048 D64, 2 of
 // B1 H16 N8192 D128 causal) and leaves whole the benchmark shapes that fill the GPU (B2 H8 N2048
 // at D 64 and 128, causal or not; B1 H16 at N 512-8192 causal; B8 H12 N1024 D64 causal).
 // FA_FORCE_SPLITS (test-only) forces S; fa_workspace_bytes and fa_forward must see the same
 // value.
 constexpr int kMaxSplits = 16;
+constexpr int kModelCus = 256;
 int s5_splits(const fa_params& p, int dtype) {
   if (const int f = env_positive_int("FA_FORCE_SPLITS")) return std::min(f, kMaxSplits);
   if (p.B < 1 || p.H < 1 || p.N < 1) return 1;
   const int bc = auto_bc_s5(p);
-  const int br = auto_br_s5(s5_list(dtype), p, bc);
-  const double cus = static_cast<double>(current_device_cus());
+  const int br = auto_br_s5(s5_list(dtype), p, bc, kModelCus);
+  const double cus = static_cast<double>(kModelCus);
   const long long n_qt = (p.N + br - 1) / br;
   const long long longest = (p.N + bc - 1) / bc;
   long long steps_per_head = 0;
@@ -400,7 +403,7 @@ int forward(int dtype, const void* q, const void* k, const void* v, void* o, flo
   const int bc = dbg.block_n != 0 ? dbg.block_n : auto_bc_s5(p);
   KArgs a = make_args(q, k, v, o, lse, p, st);
   const VariantList list = s5_list(dtype);
-  const int br = dbg.block_m != 0 ? dbg.block_m : auto_br_s5(list, p, bc);
+  const int br = dbg.block_m != 0 ? dbg.block_m : auto_br_s5(list, p, bc, current_device_cus());
   // With a workspace (fa_workspace_bytes > 0) the key walks may be split; without one the
   // whole-walk kernel runs.
   const int splits = workspace != nullptr ? s5_splits(p, dtype) : 1;

@@ -74,7 +74,8 @@ def _split_bytes(splits, rows, d):
 
 def test_stage5_split_workspace(monkeypatch):
     """Stage 5 asks for a workspace (fp32 partial O [S, B, H, N, D] + LSE [S, B, H, N]) only where
-    its cost model splits the key walks. Without a device the model assumes 256 CUs (MI355X):
+    its cost model splits the key walks. The model assumes MI355X's 256 CUs on any device (the
+    size must not depend on which device is current):
     one GPU's share of C64 over 8 GPUs (B2 H1) and of LONG (B1 H2 N8192 causal) split in two,
     the whole benchmark shapes and the GPT-2 attention shape do not."""
     monkeypatch.delenv("FA_FORCE_SPLITS", raising=False)
