@@ -382,6 +382,63 @@ def gpt_block_line(torch):
     return out
 
 
+# The reference's published benchmark grid (ref:README.md:76-135, fp16): B1 H8 and B8 H32 at
+# N 128..4096 and D 64 / 128, plus B2 H8 N2048, each dense and causal.
+GRID = ([(1, 8, n, d) for n in (128, 256, 512, 1024, 2048, 4096) for d in (64, 128)]
+        + [(8, 32, n, d) for n in (128, 256, 512, 1024, 2048, 4096) for d in (64, 128)]
+        + [(2, 8, 2048, 64), (2, 8, 2048, 128)])
+
+
+def grid_rows(torch, capi, reps=30, warmup=5):
+    """Stage 5 (C-ABI, with the workspace the library asks for) and torch SDPA on the reference's
+    grid, fp16, dense and causal. Both are timed the same way: back-to-back launches on one
+    stream, one event pair per launch, the median. Each row is gated against the fp64 oracle
+    first. Yields one dict per (config, causal)."""
+    import torch.nn.functional as F
+
+    for b, h, n, d in GRID:
+        for causal in (False, True):
+            scale = 1.0 / math.sqrt(d)
+            stream = torch.cuda.Stream()
+            # Inputs are made on the launch stream and complete before any launch reads them.
+            with torch.cuda.stream(stream):
+                sets = [make_inputs(torch, b, h, n, d, torch.float16, 1.0, seed) for seed in (0, 1)]
+                outs = [(torch.empty_like(q), torch.empty(b, h, n, device="cuda"))
+                        for q, _, _ in sets]
+                five = [(q, k, v, o, lse) for (q, k, v), (o, lse) in zip(sets, outs)]
+                attach_workspaces(torch, capi, five, causal, scale, 5)
+            stream.synchronize()
+            gate(torch, capi, *five[0], causal, scale, 5, stream)
+
+            def fused(i):
+                q, k, v, o, lse = five[i % 2]
+                capi.forward(5, q, k, v, o, lse, causal, scale, stream=stream,
+                             workspace=workspace_of(o))
+
+            def sdpa(i):
+                q, k, v = sets[i % 2]
+                F.scaled_dot_product_attention(q, k, v, is_causal=causal, scale=scale)
+
+            row = {"config": f"B{b}_H{h}_N{n}_D{d}", "causal": causal}
+            for name, fn in (("fused_ms", fused), ("sdpa_ms", sdpa)):
+                with torch.cuda.stream(stream):
+                    for i in range(warmup):
+                        fn(i)
+                    ev = [(torch.cuda.Event(enable_timing=True),
+                           torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+                    for i, (e0, e1) in enumerate(ev):
+                        e0.record(stream)
+                        fn(i)
+                        e1.record(stream)
+                stream.synchronize()
+                row[name] = sorted(e0.elapsed_time(e1) for e0, e1 in ev)[reps // 2]
+            f = flops(b, h, n, d, causal)
+            row["fused_tflops"] = f / (row["fused_ms"] * 1e-3) / 1e12
+            row["fused_pct_of_sdpa_time"] = 100.0 * row["sdpa_ms"] / row["fused_ms"]
+            del sets, outs, five
+            yield row
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -395,6 +452,10 @@ def main(argv=None) -> int:
                          "(for profiler runs)")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="CPU seconds (threads x wall) of CPU-baseline work to time")
+    ap.add_argument("--grid", action="store_true",
+                    help="the reference's benchmark grid instead of the bench line: stage 5 and "
+                         "torch SDPA per config (fp16, dense and causal), one JSON line each, "
+                         "then a markdown table")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="calibration only: launch a plain device-to-device copy of MIB MiB a few "
                          "times and exit (the known-size reference for rocprofv3 FETCH_SIZE / "
@@ -414,6 +475,19 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py: no HIP device visible", file=sys.stderr)
         return 2
+    if a.grid:
+        rows = []
+        for row in grid_rows(torch, capi):
+            print(json.dumps({k: (round(v, 5) if isinstance(v, float) else v)
+                              for k, v in row.items()}), flush=True)
+            rows.append(row)
+        print("| config | causal | fused ms | TFLOP/s | torch SDPA ms | fused, % of SDPA |")
+        print("|---|---|---|---|---|---|")
+        for r in rows:
+            print(f"| `{r['config']}` | {int(r['causal'])} | {r['fused_ms']:.4f} | "
+                  f"{r['fused_tflops']:.0f} | {r['sdpa_ms']:.4f} | "
+                  f"{r['fused_pct_of_sdpa_time']:.0f} % |")
+        return 0
     if a.copy_probe > 0:
         n = a.copy_probe << 20
         src = torch.ones(n // 4, dtype=torch.int32, device="cuda")
