@@ -289,17 +289,28 @@ bool short_walk_s5(const fa_params& p) {
   return (p.causal ? tiles + 1 : 2 * tiles) < 16;  // twice the average
 }
 
-// Stage-5 key-tile width when FA_FORCE_BC is unset: the default, except at D = 64 for short
-// walks. There BC 64 (32 keys per wave, about 150 VGPRs) lets three 4-wave workgroups share a
-// CU instead of two, hiding more of their fixed cost. Measured on the GPT-2 attention shape
-// (B8 H12 N1024 D64 fp16 causal, BR 64): 32.5 us against 37.1 us at BC 128.
-int auto_bc_s5(const fa_params& p) {
-  return (p.D == 64 && short_walk_s5(p)) ? 64 : default_bc_mfma(p.D);
+// D = 64 with 64-row workgroups and 32 keys per wave (BR 64, BC 64): about 150 VGPRs, so three
+// 4-wave workgroups share a CU instead of two and hide more of each other's fixed cost. Taken
+// for short walks, and wherever the grid holds at least three such workgroups per CU. Measured
+// (fp16, us, against BR 128 / BC 128): the GPT-2 attention shape B8 H12 N1024 causal 32.5
+// against 37.1; B8 H32 N1024 122.9 against 138.1; B8 H32 N2048 377.6 against 394.0. C64
+// (B2 H8 N2048, two per CU) stays at BR 128 / BC 128 (26.7 against 28.2).
+bool d64_narrow_s5(const fa_params& p, long long cus) {
+  if (p.D != 64) return false;
+  if (short_walk_s5(p)) return true;
+  const long long grid64 = static_cast<long long>(p.B) * p.H * ((p.N + 63) / 64);
+  return grid64 >= 3 * cus;
+}
+
+// Stage-5 key-tile width when FA_FORCE_BC is unset. It does not depend on the height, so a
+// forced height keeps the automatic width.
+int auto_bc_s5(const fa_params& p, long long cus) {
+  return d64_narrow_s5(p, cus) ? 64 : default_bc_mfma(p.D);
 }
 
 // `cus`: the compute units to fill (the current device's for a launch).
 int auto_br_s5(VariantList list, const fa_params& p, int bc, long long cus) {
-  const bool short_walk = short_walk_s5(p);
+  const bool short_walk = short_walk_s5(p) || d64_narrow_s5(p, cus);
   for (const int br : {128, 64}) {
     if (find_variant(list, p.D, br, bc) == nullptr) continue;
     if (br == 128 && short_walk && find_variant(list, p.D, 64, bc) != nullptr) continue;
@@ -336,7 +347,7 @@ constexpr int kModelCus = 256;
 int s5_splits(const fa_params& p, int dtype) {
   if (const int f = env_positive_int("FA_FORCE_SPLITS")) return std::min(f, kMaxSplits);
   if (p.B < 1 || p.H < 1 || p.N < 1) return 1;
-  const int bc = auto_bc_s5(p);
+  const int bc = auto_bc_s5(p, kModelCus);
   const int br = auto_br_s5(s5_list(dtype), p, bc, kModelCus);
   const double cus = static_cast<double>(kModelCus);
   const long long n_qt = (p.N + br - 1) / br;
@@ -400,7 +411,7 @@ int forward(int dtype, const void* q, const void* k, const void* v, void* o, flo
   if (!supports(dtype, p.D, arch)) return static_cast<int>(hipErrorNotSupported);
   const int rc = common_stage_checks("stage5", q, k, v, o, lse, p);
   if (rc != 0) return rc;
-  const int bc = dbg.block_n != 0 ? dbg.block_n : auto_bc_s5(p);
+  const int bc = dbg.block_n != 0 ? dbg.block_n : auto_bc_s5(p, current_device_cus());
   KArgs a = make_args(q, k, v, o, lse, p, st);
   const VariantList list = s5_list(dtype);
   const int br = dbg.block_m != 0 ? dbg.block_m : auto_br_s5(list, p, bc, current_device_cus());
