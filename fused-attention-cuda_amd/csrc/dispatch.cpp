@@ -302,10 +302,28 @@ bool d64_narrow_s5(const fa_params& p, long long cus) {
   return grid64 >= 3 * cus;
 }
 
+// D = 128 with one key split of 32 keys per 32-row wave (BC 32; BR 128 is a 4-wave workgroup
+// with no key-split merge). Taken when the grid holds at least two BR-128 workgroups per CU:
+// two 4-wave workgroups then share each CU without a common barrier. Measured (fp16, us,
+// against BC 64): B8 H32 N1024 192.1 against 231.2, N2048 587.8 against 705.4, N1024 causal
+// 136.7 against 177.3, N4096 causal 1223 against 1394. C128 (B2 H8 N2048, one workgroup per CU)
+// stays at BC 64 (42.1 against 48.9). Causal long walks need four per CU: with two, the two
+// workgroups resident on a CU are tiles of equal length from two heads, so the CUs holding the
+// longest tiles hold two of them (B1 H16 N4096 causal: 123.0 against 94.3 us), where the
+// 8-wave kernel hands tiles to CUs as they free up.
+bool d128_narrow_s5(const fa_params& p, long long cus) {
+  if (p.D != 128) return false;
+  const long long grid128 = static_cast<long long>(p.B) * p.H * ((p.N + 127) / 128);
+  if (grid128 < 2 * cus) return false;
+  return !p.causal || short_walk_s5(p) || grid128 >= 4 * cus;
+}
+
 // Stage-5 key-tile width when FA_FORCE_BC is unset. It does not depend on the height, so a
-// forced height keeps the automatic width.
+// forced height keeps the automatic width (and every height runs the same key split).
 int auto_bc_s5(const fa_params& p, long long cus) {
-  return d64_narrow_s5(p, cus) ? 64 : default_bc_mfma(p.D);
+  if (d64_narrow_s5(p, cus)) return 64;
+  if (d128_narrow_s5(p, cus)) return 32;
+  return default_bc_mfma(p.D);
 }
 
 // `cus`: the compute units to fill (the current device's for a launch).
