@@ -113,6 +113,34 @@ def test_stage5_default_height_matches_forced_heights(b, h, n, d, dtype, causal,
     fused_attn.set_debug_overrides(0, 0)
 
 
+# The tile stage 5 picks by itself on grids that fill a 256-CU device (csrc/dispatch.cpp,
+# auto_bc_s5 / auto_br_s5): narrow tiles where several workgroups share a CU, except for causal
+# long walks at D = 128 with fewer than four BR-128 workgroups per CU.
+@pytest.mark.parametrize("b,h,n,d,dtype,causal,tile", [
+    (8, 32, 1024, 64, torch.float16, False, (64, 64)),      # D = 64, 16 per CU
+    (4, 32, 512, 128, torch.float16, False, (128, 32)),     # D = 128, 2 per CU
+    (4, 32, 512, 128, torch.bfloat16, True, (64, 32)),      # short causal walks
+    (2, 8, 4096, 128, torch.float16, True, (128, 64)),      # causal long walks, 2 per CU
+    (1, 16, 8192, 128, torch.bfloat16, True, (128, 32)),    # LONG: causal, 4 per CU
+], ids=["d64-large", "d128-dense", "d128-short-causal", "d128-causal-2cu", "long"])
+def test_stage5_automatic_tile_on_full_grids(b, h, n, d, dtype, causal, tile, make_qkv,
+                                             reset_overrides):
+    require(5, dtype, d)
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the expected tiles are those of a 256-CU device")
+    q, k, v = make_qkv(b, h, n, d, dtype=dtype, device="cuda", seed=9)
+    fused_attn.set_debug_overrides(0, 0)
+    o0, lse0 = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
+    fused_attn.set_debug_overrides(*tile)
+    o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
+    fused_attn.set_debug_overrides(0, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o0) and torch.equal(lse, lse0), f"the default is not {tile}"
+    head = (slice(0, 1), slice(0, 1))
+    check_against_reference(o0[head].contiguous(), q[head].contiguous(), k[head].contiguous(),
+                            v[head].contiguous(), causal, dtype, lse=lse0[head].contiguous())
+
+
 @pytest.mark.parametrize("stage", [1, 2])
 def test_unbuilt_stages_raise_not_implemented(stage, make_qkv):
     if not fused_attn.is_available():
