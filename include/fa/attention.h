@@ -107,8 +107,11 @@ FA_API bool fa_impl_supports(int impl, int dtype, int D, int arch);
 
 /* Replaces fa::set_debug_overrides / get_debug_overrides (ref:include/fa/attention.cuh:60-65,
  * ref:src/dispatch.cu:177-189): forced query-tile height block_m (BR) and key-tile width block_n
- * (BC), 0 = kernel default (stage 5's default height follows the grid: the tallest of 128 / 64 /
- * 32 rows that gives every compute unit a workgroup; results do not depend on it). Process-global,
+ * (BC), 0 = kernel default. Stage 5's default height follows the grid: the tallest of 128 / 64 /
+ * 32 rows that gives every compute unit a workgroup; results do not depend on it. Its default
+ * width narrows (BC 64 at D = 64, BC 32 at D = 128) where several workgroups share a compute unit;
+ * the width changes the order of the softmax accumulation, so results move within the stated
+ * tolerance. Process-global,
  * not thread-safe (test-only). With from_env true the environment variables FA_FORCE_BR /
  * FA_FORCE_BC override the programmatic values. */
 FA_API void fa_set_debug_overrides(int block_m, int block_n);
