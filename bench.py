@@ -98,11 +98,11 @@ def make_inputs(torch, b, h, n, d, dtype, std, seed):
 _WORKSPACE = {}
 
 
-def attach_workspaces(torch, capi, sets, causal, scale, stage):
+def attach_workspaces(torch, capi, sets, causal, scale, stage, stream):
+    """Allocated on the launch stream (capi.workspace_for), and kept for the whole benchmark."""
     for q, k, _, o, _ in sets:
         nbytes = capi.workspace_bytes(stage, q, k, causal, scale)
-        _WORKSPACE[o.data_ptr()] = (torch.empty(nbytes, dtype=torch.uint8, device=q.device)
-                                    if nbytes else None)
+        _WORKSPACE[o.data_ptr()] = capi.workspace_for(stream, nbytes, q.device)
 
 
 def workspace_of(o):
@@ -291,7 +291,7 @@ def bench_workload(torch, capi, name, stage, steps, warmup, seed=0, gate_it=True
             o = torch.empty_like(q)
             lse = torch.empty(b, h, n, dtype=torch.float32, device="cuda")
             sets.append((q, k, v, o, lse))
-    attach_workspaces(torch, capi, sets, causal, scale, stage)
+    attach_workspaces(torch, capi, sets, causal, scale, stage, stream)
     stream.synchronize()
     err = gate(torch, capi, *sets[0], causal, scale, stage, stream) if gate_it else (None, None)
     eager_ms = time_steps(torch, capi, sets, causal, scale, stage, stream,
@@ -406,7 +406,7 @@ def grid_rows(torch, capi, reps=30, warmup=5):
                 outs = [(torch.empty_like(q), torch.empty(b, h, n, device="cuda"))
                         for q, _, _ in sets]
                 five = [(q, k, v, o, lse) for (q, k, v), (o, lse) in zip(sets, outs)]
-                attach_workspaces(torch, capi, five, causal, scale, 5)
+                attach_workspaces(torch, capi, five, causal, scale, 5, stream)
             stream.synchronize()
             gate(torch, capi, *five[0], causal, scale, 5, stream)
 

@@ -136,6 +136,22 @@ def workspace_bytes(impl: int, q: torch.Tensor, k: torch.Tensor, is_causal: bool
     return int(load().fa_workspace_bytes(impl, DTYPE_CODES.get(q.dtype, -1), ctypes.byref(p)))
 
 
+def workspace_for(stream: torch.cuda.Stream, nbytes: int,
+                  device: torch.device) -> torch.Tensor | None:
+    """A workspace of ``nbytes`` for a launch on ``stream`` (None for 0 bytes).
+
+    Lifetime rule: it is allocated *on the launch stream*. The caching allocator keeps a freed
+    block in the pool of the stream it was allocated on and hands it out again only to later
+    allocations on that stream, whose work the stream orders after the launch. A caller may
+    therefore drop the tensor as soon as the launch is queued. Allocated on another stream (for
+    instance torch's current one while the launch goes to ``stream``), its bytes could be reused
+    while the kernel still writes them."""
+    if not nbytes:
+        return None
+    with torch.cuda.stream(stream):
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
 def forward(impl: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
             lse: torch.Tensor | None, is_causal: bool, scale: float,
             stream: torch.cuda.Stream | None = None,
@@ -143,13 +159,13 @@ def forward(impl: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: tor
     """``fa_forward`` on torch device tensors (caller-allocated o and lse, like any C caller).
     Launches on ``stream`` (default: torch's current stream) and returns the hipError_t value.
     ``workspace``: "auto" allocates the bytes ``fa_workspace_bytes`` asks for (none for most
-    problems), None passes a null workspace, a tensor is passed as is."""
+    problems) on the launch stream (see ``workspace_for``), None passes a null workspace, a
+    tensor is passed as is."""
     b, h, n, d = q.shape
     p = params(b, h, k.shape[1], n, d, scale, is_causal)
     s = stream if stream is not None else torch.cuda.current_stream(q.device)
     if isinstance(workspace, str):
-        nbytes = workspace_bytes(impl, q, k, is_causal, scale)
-        workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
+        workspace = workspace_for(s, workspace_bytes(impl, q, k, is_causal, scale), q.device)
     ws = 0 if workspace is None else workspace.data_ptr()
     return forward_raw(impl, DTYPE_CODES[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
                        o.data_ptr(), 0 if lse is None else lse.data_ptr(), ws, p, s.cuda_stream)
@@ -169,8 +185,7 @@ def forward_strided(impl: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
     p = params(b, h, k.shape[1], n, d, scale, is_causal)
     s = stream if stream is not None else torch.cuda.current_stream(q.device)
     if isinstance(workspace, str):
-        nbytes = workspace_bytes(impl, q, k, is_causal, scale)
-        workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
+        workspace = workspace_for(s, workspace_bytes(impl, q, k, is_causal, scale), q.device)
     qs, ks, vs, os_ = strides_of(q), strides_of(k), strides_of(v), strides_of(o)
     return load().fa_forward_strided(impl, DTYPE_CODES[q.dtype], q.data_ptr(), ctypes.byref(qs),
                                      k.data_ptr(), ctypes.byref(ks), v.data_ptr(),
@@ -190,14 +205,16 @@ def decode_params(q: torch.Tensor, k: torch.Tensor, is_causal: bool, scale: floa
 def decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, lse: torch.Tensor,
            is_causal: bool, scale: float, num_splits: int = 0, workspace: torch.Tensor | None = None,
            stream: torch.cuda.Stream | None = None) -> int:
-    """``fa_decode`` on torch device tensors; allocates the workspace the library asks for unless
-    one is given. Returns the hipError_t value."""
+    """``fa_decode`` on torch device tensors; allocates the workspace the library asks for on the
+    launch stream (see ``workspace_for``) unless one is given. Returns the hipError_t value."""
     lib = load()
     p = decode_params(q, k, is_causal, scale, num_splits)
+    s = stream if stream is not None else torch.cuda.current_stream(q.device)
     if workspace is None:
         nbytes = lib.fa_decode_workspace_bytes(DTYPE_CODES.get(q.dtype, -1), ctypes.byref(p))
-        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
-    s = stream if stream is not None else torch.cuda.current_stream(q.device)
+        workspace = workspace_for(s, nbytes, q.device)
     return lib.fa_decode(DTYPE_CODES.get(q.dtype, -1), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                         o.data_ptr(), lse.data_ptr(), workspace.data_ptr(), ctypes.byref(p),
+                         o.data_ptr(), lse.data_ptr(),
+                         None if workspace is None else workspace.data_ptr(), ctypes.byref(p),
                          s.cuda_stream)
+
