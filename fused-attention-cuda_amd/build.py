@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """Build libfa_hip.so (the C-ABI kernel library) and fused_attn/_C.so (the torch binding) in-tree.
 
-  libfa_hip.so  hipcc --offload-arch=gfx950: csrc/dispatch.cpp + csrc/attn_{f16,bf16,f32}.hip.
+  libfa_hip.so  hipcc --offload-arch=gfx950: csrc/dispatch.cpp + csrc/attn_{f16,bf16,f32}.hip +
+                csrc/scratch.hip.
                 Exports exactly the functions of include/fa/attention.h.
   _C.so         csrc/ext.cpp against PyTorch-ROCm, linked to libfa_hip.so (rpath $ORIGIN).
   bench/fa_bench  the torch-free benchmark binary (bench/fa_bench.hip), linked to libfa_hip.so.
@@ -41,7 +42,7 @@ MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 HIP_FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
              "-Wall", "-Wno-unused-function",
              f"-I{INCLUDE}", f"-I{CSRC}", *NO_PACKED_FP32, *MFMA_VGPR]
-HIP_SOURCES = ["attn_f16.hip", "attn_bf16.hip", "attn_f32.hip"]
+HIP_SOURCES = ["attn_f16.hip", "attn_bf16.hip", "attn_f32.hip", "scratch.hip"]
 HOST_SOURCES = ["dispatch.cpp"]
 
 

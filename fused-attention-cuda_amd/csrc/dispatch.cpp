@@ -637,6 +637,30 @@ int fa_decode(int dtype, const void* q, const void* k, const void* v, void* o, f
   return fn(a, stream);
 }
 
+int fa_decode_noalloc(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+                      const fa_decode_params* p, hipStream_t stream) {
+  if (const char* why = fa::decode_invalid(dtype, q, k, v, o, lse, p)) {
+    if (fa::verbose()) std::fprintf(stderr, "fa_decode_noalloc: invalid params: %s\n", why);
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  const size_t need = fa_decode_workspace_bytes(dtype, p);
+  if (need > FA_DECODE_SCRATCH_BYTES) {
+    if (fa::verbose()) {
+      std::fprintf(stderr,
+                   "fa_decode_noalloc: the %d splits need %zu bytes of partials, more than the "
+                   "%u-byte scratch; ask for fewer splits or use fa_decode with a workspace\n",
+                   fa_decode_num_splits(p), need, FA_DECODE_SCRATCH_BYTES);
+    }
+    return static_cast<int>(hipErrorInvalidValue);
+  }
+  void* scratch = nullptr;
+  if (need > 0) {
+    const int rc = fa::decode_scratch(&scratch);
+    if (rc != 0) return rc;
+  }
+  return fa_decode(dtype, q, k, v, o, lse, scratch, p, stream);
+}
+
 int fa_current_arch(int* arch) {
   if (arch == nullptr) return static_cast<int>(hipErrorInvalidValue);
   int dev = 0;

@@ -102,6 +102,9 @@ struct DecArgs {
   int causal; // bottom-right: token i sees keys j <= Nkv - Nq + i
 };
 using DecodeFn = int (*)(const DecArgs& a, hipStream_t stream);
+// Device address of this GPU's FA_DECODE_SCRATCH_BYTES scratch array (scratch.hip), looked up on
+// the first call per device. Returns a hipError_t value.
+int decode_scratch(void** out);
 DecodeFn decode_f16(int D);   // attn_f16.hip; nullptr for an unsupported D
 DecodeFn decode_bf16(int D);  // attn_bf16.hip
 

@@ -31,7 +31,10 @@ DTYPE_CODES = {torch.float32: FA_DTYPE_F32, torch.float16: FA_DTYPE_F16,
 EXPORTS = ("fa_forward", "fa_forward_strided", "fa_workspace_bytes", "fa_impl_supports",
            "fa_set_debug_overrides", "fa_get_debug_overrides", "fa_impl_name", "fa_dtype_name",
            "fa_dtype_size", "fa_current_arch", "fa_error_string", "fa_decode_num_splits",
-           "fa_decode_workspace_bytes", "fa_decode")
+           "fa_decode_workspace_bytes", "fa_decode", "fa_decode_noalloc")
+
+# FA_DECODE_SCRATCH_BYTES of include/fa/attention.h: the scratch behind fa_decode_noalloc.
+DECODE_SCRATCH_BYTES = 16 << 20
 
 
 class FaParams(ctypes.Structure):
@@ -99,6 +102,8 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     lib.fa_decode_workspace_bytes.restype = ctypes.c_size_t
     lib.fa_decode.argtypes = [ci, vp, vp, vp, vp, vp, vp, dp, vp]
     lib.fa_decode.restype = ci
+    lib.fa_decode_noalloc.argtypes = [ci, vp, vp, vp, vp, vp, dp, vp]
+    lib.fa_decode_noalloc.restype = ci
     lib.fa_error_string.argtypes = [ci]
     lib.fa_error_string.restype = ctypes.c_char_p
     if path is None:
@@ -218,3 +223,16 @@ def decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, l
                          None if workspace is None else workspace.data_ptr(), ctypes.byref(p),
                          s.cuda_stream)
 
+
+def decode_noalloc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+                   lse: torch.Tensor, is_causal: bool, scale: float, num_splits: int = 0,
+                   stream: torch.cuda.Stream | None = None) -> int:
+    """``fa_decode_noalloc``: the decode with its split partials in the library's per-GPU scratch
+    array (``DECODE_SCRATCH_BYTES``) -- nothing is allocated, here or in the library. Calls that
+    may overlap on one GPU share that array and must be serialised. Returns the hipError_t
+    value."""
+    p = decode_params(q, k, is_causal, scale, num_splits)
+    s = stream if stream is not None else torch.cuda.current_stream(q.device)
+    return load().fa_decode_noalloc(DTYPE_CODES.get(q.dtype, -1), q.data_ptr(), k.data_ptr(),
+                                    v.data_ptr(), o.data_ptr(), lse.data_ptr(), ctypes.byref(p),
+                                    s.cuda_stream)

@@ -170,6 +170,23 @@ FA_API size_t fa_decode_workspace_bytes(int dtype, const fa_decode_params* p);
 FA_API int fa_decode(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
                      void* workspace, const fa_decode_params* p, hipStream_t stream);
 
+/* Bytes of device scratch behind fa_decode_noalloc: one fixed array per GPU, held from the moment
+ * the library's code is loaded on that GPU until the process ends. */
+#define FA_DECODE_SCRATCH_BYTES (16u << 20)
+
+/* fa_decode with no workspace argument and no allocation of any kind: the splits' partial O and
+ * LSE go to the library's device-resident scratch array (FA_DECODE_SCRATCH_BYTES per GPU) instead
+ * of a caller workspace. No counterpart in the reference. It is for callers that cannot allocate
+ * device memory: code under HIP graph capture, serving loops and harnesses that forbid hipMalloc.
+ * Same contract and results as fa_decode otherwise (the same kernels run). Returns
+ * hipErrorInvalidValue, before any launch, when fa_decode_workspace_bytes(dtype, p) exceeds
+ * FA_DECODE_SCRATCH_BYTES (ask for fewer splits, or use fa_decode with a workspace). Every call on
+ * one GPU shares that GPU's array: calls that may overlap on one GPU (different streams, or
+ * different host threads) race and must be serialised by the caller. The first call on each GPU
+ * looks up the array's device address (hipGetSymbolAddress, no allocation). */
+FA_API int fa_decode_noalloc(int dtype, const void* q, const void* k, const void* v, void* o,
+                             float* lse, const fa_decode_params* p, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
