@@ -32,7 +32,6 @@
 // Exit codes (ref:bench/bench_main.cu:25-26): 0 ok; 1 HIP error or failed check; 2 usage;
 // 3 stage not implemented for this (dtype, D, arch); 4 inputs do not fit in device memory.
 #include <hip/hip_runtime.h>
-#include <sys/stat.h>
 
 #include <algorithm>
 #include <cmath>
@@ -40,7 +39,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <filesystem>
 #include <string>
+#include <system_error>
 #include <utility>
 #include <vector>
 
@@ -69,12 +70,17 @@ constexpr const char* kCsvHeader =
   } while (0)
 
 // ---- device side: input fill and clock probe ------------------------------------------------
-// murmur3's 32-bit finaliser as a counter hash: element i of the tensor with `seed`.
-__device__ __forceinline__ uint32_t mix32(uint32_t x) {
+// Counter-based input generator: element i of a tensor filled with `seed` is a pure function of
+// (i, seed), so every set is reproducible and no state is shared between threads. The 64-bit
+// counter is folded with the seed by a Weyl step (golden-ratio increment) and then scrambled by
+// the "lowbias32" integer hash (C. Wellons' hash-prospector, an xor-shift-multiply sequence).
+__device__ __forceinline__ uint32_t scramble(uint64_t i, uint32_t seed) {
+  uint32_t x = static_cast<uint32_t>(i) + static_cast<uint32_t>(i >> 32) * 0x9e3779b9u +
+               seed * 0x632be5abu;
   x ^= x >> 16;
-  x *= 0x85ebca6bu;
-  x ^= x >> 13;
-  x *= 0xc2b2ae35u;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
   x ^= x >> 16;
   return x;
 }
@@ -84,13 +90,14 @@ __device__ __forceinline__ T cvt(float f) {
   return static_cast<T>(f);
 }
 
+// Uniform in [-1, 1): the top 24 bits of the hash as a fraction, then shifted.
 template <typename T>
 __global__ void fill_uniform(T* p, std::size_t n, uint32_t seed) {
-  const std::size_t stride = static_cast<std::size_t>(gridDim.x) * blockDim.x;
-  for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-       i += stride) {
-    const uint32_t r = mix32(static_cast<uint32_t>(i) ^ mix32(seed + static_cast<uint32_t>(i >> 32)));
-    p[i] = cvt<T>(static_cast<float>(r >> 8) * (2.0f / 16777216.0f) - 1.0f);
+  const std::size_t step = static_cast<std::size_t>(gridDim.x) * blockDim.x;
+  std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (; i < n; i += step) {
+    const float u = ldexpf(static_cast<float>(scramble(i, seed) >> 8), -24);  // [0, 1)
+    p[i] = cvt<T>(2.0f * u - 1.0f);
   }
 }
 
@@ -267,11 +274,15 @@ int clock_mhz(hipStream_t s) {
   return h[1] > 0 ? static_cast<int>(std::lround(static_cast<double>(h[0]) / h[1] * 100.0)) : 0;
 }
 
-double quantile(const std::vector<float>& sorted, double q) {
-  const double pos = q * static_cast<double>(sorted.size() - 1);
-  const std::size_t lo = static_cast<std::size_t>(pos);
-  const std::size_t hi = std::min(lo + 1, sorted.size() - 1);
-  return sorted[lo] + (pos - static_cast<double>(lo)) * (sorted[hi] - sorted[lo]);
+// The p-th quantile (0 <= p <= 1) of ascending `sorted`, interpolated linearly between the two
+// order statistics around rank p (n - 1) -- numpy's default definition.
+double quantile(const std::vector<float>& sorted, double p) {
+  const double rank = p * static_cast<double>(sorted.size() - 1);
+  const double below = std::floor(rank);
+  const std::size_t k = static_cast<std::size_t>(below);
+  if (k + 1 >= sorted.size()) return sorted.back();
+  const double lo = sorted[k], hi = sorted[k + 1];
+  return lo + (rank - below) * (hi - lo);
 }
 
 volatile uint64_t g_sink = 0;
@@ -288,17 +299,21 @@ std::string fmt(const char* f, double v) {
   return buf;
 }
 
-std::string csv_field(const std::string& s) {
-  if (s.find_first_of(",\"\n") == std::string::npos) return s;
-  std::string q = "\"";
-  for (char c : s) q += c == '"' ? std::string("\"\"") : std::string(1, c);
-  return q + "\"";
+// One CSV field (RFC 4180): text with a comma, quote or line break is quoted, quotes doubled.
+std::string csv_field(const std::string& text) {
+  if (text.find_first_of(",\"\n") == std::string::npos) return text;
+  std::string quoted = text;
+  for (std::size_t at = quoted.find('"'); at != std::string::npos; at = quoted.find('"', at + 2)) {
+    quoted.insert(at, 1, '"');
+  }
+  return '"' + quoted + '"';
 }
 
+// Creates the directories above `path` (the file itself is not created).
 void mkdir_parents(const std::string& path) {
-  for (std::size_t i = 1; i < path.size(); ++i) {
-    if (path[i] == '/') mkdir(path.substr(0, i).c_str(), 0755);
-  }
+  const std::filesystem::path dir = std::filesystem::path(path).parent_path();
+  std::error_code ignored;
+  if (!dir.empty()) std::filesystem::create_directories(dir, ignored);
 }
 
 // Prints header + row, and appends the row to --out (header first when the file is new).
@@ -441,14 +456,16 @@ int run(const Options& opt, const DeviceInfo& dev, hipStream_t stream) {
   const std::size_t ws_bytes = fa_workspace_bytes(opt.stage, dt, &p);
   const std::size_t set_bytes = q_bytes + 2 * kv_bytes;
   const std::size_t fixed = q_bytes + lse_bytes + ws_bytes + kFlushBytes;
-  const std::size_t budget = dev.free - dev.free / 10;
-  int nsets = kMaxSets;
-  while (nsets > 1 && fixed + static_cast<std::size_t>(nsets) * set_bytes > budget) --nsets;
-  if (fixed + set_bytes > budget) {
-    std::fprintf(stderr, "inputs do not fit: need %.2f GB, budget %.2f GB\n",
-                 (fixed + set_bytes) / 1e9, budget / 1e9);
+  // Rotating input sets: as many as fit (at most kMaxSets) in 90 % of the free memory after the
+  // buffers every launch shares (O, LSE, workspace, the flush buffer).
+  const std::size_t usable = dev.free / 10 * 9;
+  const std::size_t room = usable > fixed ? usable - fixed : 0;
+  if (room < set_bytes) {
+    std::fprintf(stderr, "inputs do not fit: need %.2f GB, %.2f GB usable\n",
+                 (fixed + set_bytes) / 1e9, usable / 1e9);
     return kNoMemory;
   }
+  const int nsets = static_cast<int>(std::min<std::size_t>(kMaxSets, room / set_bytes));
   std::vector<std::string> notes;
   if (opt.smoke) notes.push_back("smoke");
   if (p.causal) notes.push_back("flops=causal_half");

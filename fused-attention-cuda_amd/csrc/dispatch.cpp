@@ -342,6 +342,21 @@ VariantList s5_list(int dtype) {
   return dtype == FA_DTYPE_F16 ? variants_s5_f16() : variants_s5_bf16();
 }
 
+// Width paired with a forced height (FA_FORCE_BR without FA_FORCE_BC): the automatic width when
+// (BR, width) is instantiated, so that a forced height computes the default's rows bit for bit;
+// otherwise the default width, then the widest instantiated one, so that a forced height alone is
+// valid on every grid. The width only ever changes the order of the accumulation. A height with no
+// instantiated width at all keeps the automatic one (and the launch reports the invalid tile).
+int width_for_forced_height(VariantList list, int D, int br, int auto_bc) {
+  if (find_variant(list, D, br, auto_bc) != nullptr) return auto_bc;
+  if (find_variant(list, D, br, default_bc_mfma(D)) != nullptr) return default_bc_mfma(D);
+  int widest = 0;
+  for (int i = 0; i < list.n; ++i) {
+    if (list.v[i].D == D && list.v[i].br == br) widest = std::max(widest, list.v[i].bc);
+  }
+  return widest != 0 ? widest : auto_bc;
+}
+
 // Split key walks (stage 5, with a workspace). When the grid leaves CUs idle, or a causal
 // problem's longest key walk is far above the average work per CU, the critical path is one
 // workgroup's walk. Cutting every walk into S parts of whole tiles (one workgroup each; the parts'
@@ -429,9 +444,10 @@ int forward(int dtype, const void* q, const void* k, const void* v, void* o, flo
   if (!supports(dtype, p.D, arch)) return static_cast<int>(hipErrorNotSupported);
   const int rc = common_stage_checks("stage5", q, k, v, o, lse, p);
   if (rc != 0) return rc;
-  const int bc = dbg.block_n != 0 ? dbg.block_n : auto_bc_s5(p, current_device_cus());
-  KArgs a = make_args(q, k, v, o, lse, p, st);
   const VariantList list = s5_list(dtype);
+  int bc = dbg.block_n != 0 ? dbg.block_n : auto_bc_s5(p, current_device_cus());
+  if (dbg.block_m != 0 && dbg.block_n == 0) bc = width_for_forced_height(list, p.D, dbg.block_m, bc);
+  KArgs a = make_args(q, k, v, o, lse, p, st);
   const int br = dbg.block_m != 0 ? dbg.block_m : auto_br_s5(list, p, bc, current_device_cus());
   // With a workspace (fa_workspace_bytes > 0) the key walks may be split; without one the
   // whole-walk kernel runs.

@@ -1,27 +1,16 @@
-"""fused_attn -- MI355X-native fused SDPA forward behind the reference's ``torch.ops.fused_attn`` API.
+"""fused_attn: the ``torch.ops.fused_attn`` operators, backed by gfx950 (MI355X) HIP kernels.
 
-Same public surface as the reference package (ref:python/fused_attn/__init__.py:1-119):
-``forward``, ``forward_stage``, ``impl_supports``, ``impl_name``, ``set_debug_overrides``,
-``is_available`` and the ``ops`` module with the fake kernels. The ops are registered by the
-compiled binding ``_C`` (csrc/ext.cpp), which calls the gfx950 kernels through the C-ABI of
-``libfa_hip.so`` (include/fa/attention.h); :mod:`fused_attn.capi` binds that C-ABI with ctypes.
+The public names and signatures are the reference package's (ref:python/fused_attn/__init__.py:
+1-119): ``forward``, ``forward_stage``, ``impl_supports``, ``impl_name``, ``set_debug_overrides``,
+``is_available`` and the ``ops`` module. Two operators extend that surface: ``forward_strided``
+(strided [B, H, N, D] views, no copies) and ``decode`` (split-KV decode).
 
-Import always succeeds; calling an op without the compiled extension raises ``ImportError`` with
-the build command -- there is no CPU or eager fallback.
+Layers: the compiled module ``_C`` (csrc/ext.cpp) defines the operators with the reference's
+schemas and calls ``libfa_hip.so`` through its C-ABI (include/fa/attention.h); :mod:`.ops` holds
+their meta kernels; :mod:`.capi` binds the C-ABI directly with ctypes.
 
-Build (from the repo root)::
-
-    python fused-attention-cuda_amd/build.py
-
-Ops (schemas as in the reference, ref:python/fused_attn/ext.cpp:220-230)::
-
-    torch.ops.fused_attn.forward(q, k, v, is_causal, scale) -> Tensor
-    torch.ops.fused_attn.forward_stage(q, k, v, is_causal, scale, stage) -> (Tensor, Tensor)
-
-plus two extensions with no counterpart in the reference:
-``torch.ops.fused_attn.forward_strided(q, k, v, is_causal, scale) -> Tensor`` over strided views,
-and ``torch.ops.fused_attn.decode(q, k, v, is_causal, scale, num_splits) -> (Tensor, Tensor)``,
-split-KV decode of Nq new tokens against Nkv cached keys (the reference's stated next step).
+Importing this package never fails. If ``_C`` did not load, every operator call raises
+``ImportError`` naming the build command; nothing falls back to another implementation.
 """
 
 from __future__ import annotations
@@ -47,94 +36,95 @@ __all__ = [
 ]
 __version__ = "0.1.0"
 
-_EXT_ERROR: ImportError | None
-try:
-    from . import _C  # noqa: F401  (loading the .so runs the TORCH_LIBRARY static initialisers)
-except ImportError as exc:  # pragma: no cover - depends on the machine
-    _EXT_ERROR = exc
-else:
-    _EXT_ERROR = None
-    ops.register_fakes()
 
-_BUILD_HINT = (
-    "fused_attn._C is not built. From the repo root run\n"
-    "  python fused-attention-cuda_amd/build.py\n"
-    "(needs hipcc from ROCm and a ROCm build of PyTorch; the kernels target gfx950 / MI355X)."
-)
+class _Binding:
+    """The compiled operator library, or why it is missing."""
 
-_DTYPE_NAMES = {torch.float32: "fp32", torch.float16: "fp16", torch.bfloat16: "bf16"}
+    BUILD_COMMAND = "python fused-attention-cuda_amd/build.py"
+
+    def __init__(self) -> None:
+        self.missing: ImportError | None = None
+        try:
+            # Loading the shared object runs its TORCH_LIBRARY registration.
+            from . import _C  # noqa: F401
+        except ImportError as exc:  # pragma: no cover - depends on the build
+            self.missing = exc
+        else:
+            ops.register_fakes()
+
+    def library(self):
+        """``torch.ops.fused_attn``, or ImportError with the build instructions."""
+        if self.missing is not None:
+            raise ImportError(
+                "the fused_attn HIP extension (fused_attn/_C.so) is not built; build it from the "
+                f"repository root with `{self.BUILD_COMMAND}` (hipcc from ROCm, a ROCm build of "
+                "PyTorch; the kernels are compiled for gfx950)") from self.missing
+        return torch.ops.fused_attn
+
+
+_BINDING = _Binding()
+_DTYPE_TAGS = {torch.float32: "fp32", torch.float16: "fp16", torch.bfloat16: "bf16"}
 
 
 def is_available() -> bool:
-    """True when the compiled extension imported."""
-    return _EXT_ERROR is None
+    """Whether the compiled extension loaded."""
+    return _BINDING.missing is None
 
 
-def _require_ext() -> None:
-    if _EXT_ERROR is not None:
-        raise ImportError(_BUILD_HINT) from _EXT_ERROR
-
-
-def _resolve_scale(q: Tensor, scale: float | None) -> float:
-    # PyTorch's SDPA default; the one place the default is decided.
-    return float(1.0 / math.sqrt(q.shape[-1]) if scale is None else scale)
+def _softmax_scale(q: Tensor, scale: float | None) -> float:
+    """The scale the operators get: the caller's, else 1/sqrt(D) as in torch's SDPA. The
+    operators themselves have no default, so this is the only place one is chosen."""
+    return 1.0 / math.sqrt(q.shape[-1]) if scale is None else float(scale)
 
 
 def forward(q: Tensor, k: Tensor, v: Tensor, is_causal: bool = False,
             scale: float | None = None) -> Tensor:
-    """Fused attention forward, dispatched to the best implemented stage for (dtype, D, GPU)."""
-    _require_ext()
-    return torch.ops.fused_attn.forward(q, k, v, bool(is_causal), _resolve_scale(q, scale))
+    """softmax(scale * q k^T) v for q [B, H, N, D] and k, v [B, Hkv, N, D] (top-left causal mask
+    when ``is_causal``), on the highest stage built for (dtype, D) on this GPU."""
+    return _BINDING.library().forward(q, k, v, bool(is_causal), _softmax_scale(q, scale))
 
 
 def forward_stage(q: Tensor, k: Tensor, v: Tensor, stage: int, is_causal: bool = False,
                   scale: float | None = None) -> tuple[Tensor, Tensor]:
-    """Run one explicit stage (1..5). Returns ``(o, lse)``; ``lse`` is empty for stages 1-2."""
-    _require_ext()
-    return torch.ops.fused_attn.forward_stage(q, k, v, bool(is_causal),
-                                              _resolve_scale(q, scale), int(stage))
+    """The forward on one named stage (1..5), returning (O, LSE); LSE is fp32 [B, H, N] (the row
+    log-sum-exp, natural log) for stages 3-5 and empty for the materialising stages 1-2."""
+    return _BINDING.library().forward_stage(q, k, v, bool(is_causal), _softmax_scale(q, scale),
+                                            int(stage))
 
 
 def forward_strided(q: Tensor, k: Tensor, v: Tensor, is_causal: bool = False,
                     scale: float | None = None) -> Tensor:
-    """``forward`` over strided [B, H, N, D] views (head dim contiguous, batch/head/row strides
-    multiples of 16 bytes), e.g. ``qkv.view(B, N, 3, H, D)[:, :, 0].transpose(1, 2)`` with no copy.
-    The output is dense in q's memory order (see ``ops.empty_in_layout_of``). An extension of the
-    reference op surface, which only takes contiguous tensors."""
-    _require_ext()
-    return torch.ops.fused_attn.forward_strided(q, k, v, bool(is_causal), _resolve_scale(q, scale))
+    """``forward`` on strided [B, H, N, D] views -- the head dim contiguous, every other stride a
+    multiple of 16 bytes -- such as ``qkv.view(B, N, 3, H, D)[:, :, 0].transpose(1, 2)``, read in
+    place. O comes back dense in q's memory order (``ops.empty_in_layout_of``)."""
+    return _BINDING.library().forward_strided(q, k, v, bool(is_causal), _softmax_scale(q, scale))
 
 
 def decode(q: Tensor, k: Tensor, v: Tensor, is_causal: bool = False, scale: float | None = None,
            num_splits: int = 0) -> tuple[Tensor, Tensor]:
-    """Split-KV decode: q [B, H, Nq, D] (the Nq newest tokens) against the cache k, v
-    [B, Hkv, Nkv, D] -> (o [B, H, Nq, D], lse [B, H, Nq]). With ``is_causal`` token i sees keys
-    j <= Nkv - Nq + i (bottom-right alignment). ``num_splits`` = 0 lets the library choose how
-    many pieces of the key range run in parallel; the pieces are combined with LSE weights.
-    fp16/bf16, D 64 or 128, (H / Hkv) * Nq <= 64."""
-    _require_ext()
-    return torch.ops.fused_attn.decode(q, k, v, bool(is_causal), _resolve_scale(q, scale),
-                                       int(num_splits))
+    """Split-KV decode: the Nq newest tokens q [B, H, Nq, D] against the cache k, v
+    [B, Hkv, Nkv, D], returning (O [B, H, Nq, D], LSE [B, H, Nq]). ``is_causal`` aligns the mask
+    bottom-right (token i sees keys j <= Nkv - Nq + i). The key range runs in ``num_splits``
+    parallel pieces merged by their LSE (0: the library chooses). fp16 / bf16, D 64 or 128,
+    (H / Hkv) * Nq <= 64."""
+    return _BINDING.library().decode(q, k, v, bool(is_causal), _softmax_scale(q, scale),
+                                     int(num_splits))
 
 
 def impl_supports(stage: int, dtype: torch.dtype, head_dim: int) -> bool:
-    """Whether this build can run ``stage`` for (dtype, D) on the *current* device."""
-    _require_ext()
-    name = _DTYPE_NAMES.get(dtype)
-    if name is None:
-        return False
-    return bool(torch.ops.fused_attn.impl_supports(int(stage), name, int(head_dim)))
+    """Whether ``stage`` is built for (dtype, head_dim) on the current device."""
+    library = _BINDING.library()
+    tag = _DTYPE_TAGS.get(dtype)
+    return tag is not None and bool(library.impl_supports(int(stage), tag, int(head_dim)))
 
 
 def impl_name(stage: int) -> str:
-    """ "naive" / "tiled" / "fused" / "wmma" / "tuned" (the reference's stage names)."""
-    _require_ext()
-    return str(torch.ops.fused_attn.impl_name(int(stage)))
+    """The stage's name in the reference ladder: naive, tiled, fused, wmma or tuned."""
+    return str(_BINDING.library().impl_name(int(stage)))
 
 
 def set_debug_overrides(block_m: int = 0, block_n: int = 0) -> None:
-    """TEST-ONLY: force the query-tile height (BR) and key-tile width (BC); 0 = default.
-
-    Global, process-wide, not thread-safe by design -- always reset to ``(0, 0)`` afterwards."""
-    _require_ext()
-    torch.ops.fused_attn.set_debug_overrides(int(block_m), int(block_n))
+    """For tests only: force the query-tile height (block_m, BR) and key-tile width (block_n, BC)
+    of the fused stages; 0 restores the default. The setting is process-wide and not
+    thread-safe; reset it to (0, 0) when done."""
+    _BINDING.library().set_debug_overrides(int(block_m), int(block_n))

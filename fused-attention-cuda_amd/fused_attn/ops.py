@@ -1,11 +1,19 @@
-"""Fake (meta) kernels and the opcheck helper for the ``fused_attn::*`` ops.
+"""Meta kernels of the ``fused_attn`` ops, and an ``opcheck`` driver for them.
 
-``torch.compile`` / AOTAutograd trace ops on fake tensors that carry only shape, dtype and device.
-The fakes below describe the outputs of both ops without touching data, which is what keeps
-``torch.compile(fullgraph=True)`` free of graph breaks. Behaviour follows the reference's fakes
-(ref:python/fused_attn/ops.py:28-70): the same ``torch._check`` mirrors of the C++ input checks,
-``o = empty_like(q)`` and an fp32 ``lse`` of ``[B, H, N]`` for stages 3-5 (``(0,)`` otherwise).
-The fakes are registered after ``fused_attn._C`` is loaded (the schemas live in C++).
+A meta ("fake") kernel computes the metadata of an op's outputs -- shape, dtype, device, layout --
+from the metadata of its inputs, without reading any data. ``torch.compile``, AOTAutograd and
+``FakeTensorMode`` call it in place of the HIP kernel while they trace; without one, tracing stops
+at the op (a graph break). The rules below restate what ``csrc/ext.cpp`` allocates and checks:
+
+* ``forward``       -> O shaped and typed like q;
+* ``forward_stage`` -> (O, LSE) with LSE fp32 ``[B, H, N]`` for the stages whose kernels produce
+  it (3, 4, 5) and an empty ``(0,)`` tensor for stages 1-2, the reference op's contract
+  (ref:python/fused_attn/ops.py:28-70, ref:python/fused_attn/ext.cpp:159-188);
+* ``forward_strided`` -> O dense in q's memory order;
+* ``decode``        -> (O like q, LSE fp32 ``[B, H, Nq]``).
+
+Input rules become ``torch._check`` calls, so under symbolic shapes they turn into guards rather
+than failures. The meta kernels are installed once ``fused_attn._C`` has defined the schemas.
 """
 
 from __future__ import annotations
@@ -17,113 +25,118 @@ from torch import Tensor
 
 SUPPORTED_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
 SUPPORTED_HEAD_DIMS = (64, 128)
-# Stages whose kernels write the logsumexp.
+# Stages whose kernels write the row logsumexp; the materialising stages 1-2 return an empty LSE.
 LSE_STAGES = (3, 4, 5)
 
-_registered = False
+_installed = False
 
 
-def _check_inputs(q: Tensor, k: Tensor, v: Tensor) -> None:
-    """``torch._check`` mirror of the TORCH_CHECKs in csrc/ext.cpp (each becomes a guard or a
-    runtime assert under symbolic shapes)."""
-    torch._check(q.dim() == 4 and k.dim() == 4 and v.dim() == 4, lambda: "q/k/v must be [B,H,N,D]")
-    torch._check(q.dtype == k.dtype and q.dtype == v.dtype, lambda: "q/k/v must share one dtype")
-    torch._check(q.dtype in SUPPORTED_DTYPES, lambda: f"unsupported dtype {q.dtype}")
-    b, h, n, d = q.shape
-    torch._check(d == 64 or d == 128, lambda: f"D must be 64 or 128, got {d}")
-    torch._check(n % 32 == 0, lambda: f"N must be a multiple of 32, got {n}")
-    torch._check(k.shape[0] == b and v.shape[0] == b, lambda: "batch mismatch")
-    torch._check(k.shape[2] == n and v.shape[2] == n, lambda: "Nq == Nkv is required")
-    torch._check(k.shape[3] == d and v.shape[3] == d, lambda: "head-dim mismatch")
-    torch._check(k.shape[1] == v.shape[1], lambda: "k and v must have the same number of heads")
-    torch._check(h % k.shape[1] == 0, lambda: "H must be a multiple of Hkv")
+def _rule(ok, message: str) -> None:
+    torch._check(ok, lambda: message)
 
 
-def _fake_forward(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, scale: float) -> Tensor:
-    _check_inputs(q, k, v)
+def _attention_contract(q: Tensor, k: Tensor, v: Tensor) -> None:
+    """The operand rules of ``forward``, ``forward_stage`` and ``forward_strided`` (layout and
+    alignment aside, which fake tensors do not carry); csrc/ext.cpp enforces the same ones, with
+    the same wording where a test matches it."""
+    _rule(q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "q, k and v must be 4-D [B, H, N, D]")
+    _rule(k.dtype == q.dtype and v.dtype == q.dtype, "q, k and v must have the same dtype")
+    _rule(q.dtype in SUPPORTED_DTYPES, f"dtype {q.dtype} is not supported")
+    batch, heads, n, d = q.shape
+    _rule(d == 64 or d == 128, f"D must be 64 or 128 (got {d})")
+    _rule(n % 32 == 0, f"N must be a multiple of 32 (got {n})")
+    _rule(k.shape[0] == batch and v.shape[0] == batch, "q, k and v must share the batch size")
+    _rule(k.shape[2] == n and v.shape[2] == n, "Nq == Nkv is required")
+    _rule(k.shape[3] == d and v.shape[3] == d, "q, k and v must share the head dim")
+    _rule(k.shape[1] == v.shape[1], "k and v must have the same head count")
+    _rule(heads % k.shape[1] == 0, "H must be a multiple of Hkv")
+
+
+def _meta_forward(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, scale: float) -> Tensor:
+    _attention_contract(q, k, v)
     return torch.empty_like(q)
 
 
-def _fake_forward_stage(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, scale: float,
+def _meta_forward_stage(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, scale: float,
                         stage: int) -> tuple[Tensor, Tensor]:
-    _check_inputs(q, k, v)
-    torch._check(1 <= stage <= 5, lambda: f"stage must be in 1..5, got {stage}")
-    b, h, n, _ = q.shape
-    o = torch.empty_like(q)
-    if stage in LSE_STAGES:
-        lse = q.new_empty((b, h, n), dtype=torch.float32)
-    else:
-        lse = q.new_empty((0,), dtype=torch.float32)
-    return o, lse
+    _attention_contract(q, k, v)
+    _rule(1 <= stage <= 5, f"stage must be in 1..5 (got {stage})")
+    lse_shape = tuple(q.shape[:3]) if stage in LSE_STAGES else (0,)
+    return torch.empty_like(q), q.new_empty(lse_shape, dtype=torch.float32)
 
 
 def empty_in_layout_of(q: Tensor) -> Tensor:
-    """A dense tensor of q's shape whose memory order follows q's strides (outermost first) --
-    the output layout of ``forward_strided`` (csrc/ext.cpp ``empty_in_layout_of``): for the
-    [B, H, N, D] view of a [B, N, H, D] buffer it is a [B, N, H, D] buffer seen as [B, H, N, D]."""
-    order = sorted(range(4), key=lambda d: -q.stride(d))  # stable: ties keep dimension order
-    out = q.new_empty([q.shape[d] for d in order])
-    inverse = [order.index(d) for d in range(4)]
-    return out.permute(inverse)
+    """A new dense tensor shaped like q whose memory order is q's (dimensions ranked by stride,
+    largest first; ties keep their order) -- what ``forward_strided`` allocates for O
+    (csrc/ext.cpp ``empty_in_layout_of``). For the [B, H, N, D] view of a [B, N, H, D] buffer it is
+    a [B, N, H, D] buffer seen as [B, H, N, D]."""
+    by_stride = sorted(range(q.dim()), key=lambda dim: -q.stride(dim))
+    storage_order = q.new_empty([q.shape[dim] for dim in by_stride])
+    return storage_order.permute([by_stride.index(dim) for dim in range(q.dim())])
 
 
-def _fake_forward_strided(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, scale: float) -> Tensor:
-    torch._check(q.dim() == 4 and k.dim() == 4 and v.dim() == 4, lambda: "q/k/v must be [B,H,N,D]")
-    b, h, n, d = q.shape
-    torch._check(d == 64 or d == 128, lambda: f"D must be 64 or 128, got {d}")
-    torch._check(n % 32 == 0, lambda: f"N must be a multiple of 32, got {n}")
-    torch._check(q.dtype == k.dtype and q.dtype == v.dtype, lambda: "q/k/v must share one dtype")
+def _meta_forward_strided(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
+                          scale: float) -> Tensor:
+    _attention_contract(q, k, v)
     return empty_in_layout_of(q)
 
 
-def _fake_decode(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, scale: float,
+def _meta_decode(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, scale: float,
                  num_splits: int) -> tuple[Tensor, Tensor]:
-    torch._check(q.dim() == 4 and k.dim() == 4 and v.dim() == 4,
-                 lambda: "decode expects q [B, H, Nq, D] and k, v [B, Hkv, Nkv, D]")
-    b, h, nq, d = q.shape
-    torch._check(q.dtype == k.dtype and q.dtype == v.dtype, lambda: "q/k/v must share one dtype")
-    torch._check(k.shape[1] > 0 and h % k.shape[1] == 0, lambda: "H must be a multiple of Hkv")
-    return torch.empty_like(q), q.new_empty((b, h, nq), dtype=torch.float32)
+    _rule(q.dim() == 4 and k.dim() == 4 and v.dim() == 4,
+          "decode takes q [B, H, Nq, D] and k, v [B, Hkv, Nkv, D]")
+    _rule(k.dtype == q.dtype and v.dtype == q.dtype, "q, k and v must have the same dtype")
+    _rule(k.shape[1] > 0 and q.shape[1] % k.shape[1] == 0, "H must be a multiple of Hkv")
+    return torch.empty_like(q), q.new_empty(tuple(q.shape[:3]), dtype=torch.float32)
+
+
+_META_KERNELS = {
+    "fused_attn::forward": _meta_forward,
+    "fused_attn::forward_stage": _meta_forward_stage,
+    "fused_attn::forward_strided": _meta_forward_strided,
+    "fused_attn::decode": _meta_decode,
+}
 
 
 def register_fakes() -> None:
-    """Register the fake kernels (idempotent; requires ``fused_attn._C`` to be loaded)."""
-    global _registered
-    if _registered:
-        return
-    torch.library.register_fake("fused_attn::forward", _fake_forward)
-    torch.library.register_fake("fused_attn::forward_stage", _fake_forward_stage)
-    torch.library.register_fake("fused_attn::forward_strided", _fake_forward_strided)
-    torch.library.register_fake("fused_attn::decode", _fake_decode)
-    _registered = True
+    """Install every meta kernel once (the op schemas must already exist: import ``_C`` first)."""
+    global _installed
+    if not _installed:
+        for name, kernel in _META_KERNELS.items():
+            torch.library.register_fake(name, kernel)
+        _installed = True
 
 
-# opcheck runs in two groups (ref:python/fused_attn/ops.py:73-96): the autograd-registration check
-# needs an input with requires_grad=True, while the others must see plain inputs (with grad-
-# requiring inputs the AOT check would trace a backward for an op that has no autograd kernel).
-_NO_GRAD_TESTS = ("test_schema", "test_faketensor", "test_aot_dispatch_dynamic")
-_GRAD_TESTS = ("test_autograd_registration",)
+# torch.library.opcheck utilities, and whether each one must see tensor inputs that require grad.
+# The autograd-registration check refuses to run without such an input; the AOT-dispatch check
+# must not get one, or it would trace a backward for ops that have no autograd formula.
+_OPCHECK_UTILS = {
+    "test_schema": False,
+    "test_faketensor": False,
+    "test_aot_dispatch_dynamic": False,
+    "test_autograd_registration": True,
+}
 
 
 def _opcheck(op, args: tuple) -> dict[str, str]:
-    q, k, v, *rest = args
-    res = dict(torch.library.opcheck(op, (q, k, v, *rest), test_utils=_NO_GRAD_TESTS))
-    grad_args = (q.detach().requires_grad_(), k.detach().requires_grad_(),
-                 v.detach().requires_grad_(), *rest)
-    res.update(torch.library.opcheck(op, grad_args, test_utils=_GRAD_TESTS))
-    return res
+    report: dict[str, str] = {}
+    for needs_grad in (False, True):
+        utils = tuple(u for u, g in _OPCHECK_UTILS.items() if g is needs_grad)
+        call_args = tuple(a.detach().requires_grad_() if needs_grad and isinstance(a, Tensor)
+                          else a for a in args)
+        report.update(torch.library.opcheck(op, call_args, test_utils=utils))
+    return report
 
 
 def opcheck_all(q: Tensor, k: Tensor, v: Tensor, is_causal: bool = False,
                 scale: float | None = None,
                 stages: Sequence[int] = ()) -> dict[str, dict[str, str]]:
-    """``torch.library.opcheck`` on ``forward`` and on ``forward_stage`` for each stage
-    (schema, fake vs real, AOT dispatch with dynamic shapes, autograd registration)."""
-    if scale is None:
-        scale = 1.0 / (q.shape[-1] ** 0.5)
-    results: dict[str, dict[str, str]] = {}
-    results["forward"] = _opcheck(torch.ops.fused_attn.forward, (q, k, v, is_causal, float(scale)))
+    """``torch.library.opcheck`` -- schema, meta kernel against the real one, AOT dispatch with
+    dynamic shapes, autograd registration -- on ``forward`` and on ``forward_stage`` for every
+    stage in ``stages``. Raises on the first failure; returns each op's report."""
+    scale = float(q.shape[-1] ** -0.5 if scale is None else scale)
+    report = {"forward": _opcheck(torch.ops.fused_attn.forward, (q, k, v, is_causal, scale))}
     for stage in stages:
-        results[f"forward_stage[{stage}]"] = _opcheck(
-            torch.ops.fused_attn.forward_stage, (q, k, v, is_causal, float(scale), int(stage)))
-    return results
+        report[f"forward_stage[{stage}]"] = _opcheck(
+            torch.ops.fused_attn.forward_stage, (q, k, v, is_causal, scale, int(stage)))
+    return report

@@ -111,7 +111,8 @@ FA_API bool fa_impl_supports(int impl, int dtype, int D, int arch);
  * 32 rows that gives every compute unit a workgroup; results do not depend on it. Its default
  * width narrows (BC 64 at D = 64, BC 32 at D = 128) where several workgroups share a compute unit;
  * the width changes the order of the softmax accumulation, so results move within the stated
- * tolerance. Process-global,
+ * tolerance. A forced height alone keeps the automatic width where that tile is built and
+ * otherwise takes a built width for that height, so it is valid on every grid. Process-global,
  * not thread-safe (test-only). With from_env true the environment variables FA_FORCE_BR /
  * FA_FORCE_BC override the programmatic values. */
 FA_API void fa_set_debug_overrides(int block_m, int block_n);

@@ -55,3 +55,32 @@ def check_against_reference(o, q, k, v, causal, dtype, attn_mask=None, scale=Non
     if lse is not None:
         assert_close_tol(lse, lse64, LSE_ATOL, 0.0, what="LSE")
     return r
+
+
+def fp32_reference_head(q, k, v, bi, hi, causal, scale):
+    """Plain PyTorch fp32 attention for one head, every row, on the tensors' device: the fp32
+    reference of the op. The kv head is h // (H / Hkv). Returns (O [N, D], LSE [N], scores [N, N])
+    in fp32; the scores are returned for the LSE bounds some tests check."""
+    hk = hi // (q.shape[1] // k.shape[1])
+    q32, k32, v32 = q[bi, hi].float(), k[bi, hk].float(), v[bi, hk].float()
+    s = torch.matmul(q32, k32.t().contiguous()) * scale
+    if causal:
+        n = s.shape[0]
+        s = s.masked_fill(~torch.ones(n, n, dtype=torch.bool, device=s.device).tril(),
+                          float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), v32), torch.logsumexp(s, dim=-1), s
+
+
+def assert_every_head_close(o, lse, q, k, v, causal, scale, what=""):
+    """O and LSE of every (b, h) head against the fp32 reference, to the stated tolerance."""
+    atol, rtol = O_TOL[o.dtype]
+    b, h = q.shape[:2]
+    for bi in range(b):
+        for hi in range(h):
+            o32, lse32, s = fp32_reference_head(q, k, v, bi, hi, causal, scale)
+            del s
+            err = (o[bi, hi].float() - o32).abs()
+            excess = float((err - (atol + rtol * o32.abs())).max())
+            assert excess <= 0.0, f"{what} head ({bi},{hi}): max|O err| {float(err.max()):.3e}"
+            lerr = float((lse[bi, hi] - lse32).abs().max())
+            assert lerr <= LSE_ATOL, f"{what} head ({bi},{hi}): max|LSE err| {lerr:.3e}"

@@ -1,4 +1,4 @@
-"""Shared pytest configuration (mirrors ref:tests/conftest.py).
+"""Shared pytest configuration (the roles of ref:tests/conftest.py).
 
 * Puts the repo root (for ``oracle``) and ``fused-attention-cuda_amd`` (for ``fused_attn``) on
   ``sys.path`` so a clean checkout needs no install.
@@ -27,31 +27,36 @@ STAGES = (1, 2, 3, 4, 5)
 
 def pytest_addoption(parser: pytest.Parser) -> None:
     parser.addoption("--stage", action="store", default="all",
-                     help="run stage-parametrised GPU tests for one stage only (1..5)")
+                     help="keep only this stage (1..5) of the stage-parametrised tests")
 
 
 def pytest_configure(config: pytest.Config) -> None:
     config.addinivalue_line(
-        "markers", "gpu: needs a HIP device; auto-skipped when torch.cuda.is_available() is False")
+        "markers", "gpu: needs a HIP device; skipped where torch.cuda.is_available() is False")
+
+
+def _stage_of(item: pytest.Item):
+    """The ``stage`` parameter of a parametrised test item, or None."""
+    callspec = getattr(item, "callspec", None)
+    return None if callspec is None else callspec.params.get("stage")
 
 
 def pytest_collection_modifyitems(config: pytest.Config, items: list[pytest.Item]) -> None:
-    have_gpu = torch.cuda.is_available()
-    skip_gpu = pytest.mark.skip(reason="no HIP device (torch.cuda.is_available() is False)")
-    wanted = config.getoption("--stage")
-    only_stage = None if wanted in (None, "all") else int(wanted)
-    kept, deselected = [], []
-    for item in items:
-        if "gpu" in item.keywords and not have_gpu:
-            item.add_marker(skip_gpu)
-        params = getattr(getattr(item, "callspec", None), "params", {})
-        if only_stage is not None and "stage" in params and params["stage"] != only_stage:
-            deselected.append(item)
-        else:
-            kept.append(item)
-    if deselected:
-        config.hook.pytest_deselected(items=deselected)
-        items[:] = kept
+    """Two adjustments: GPU tests are marked skipped on a machine without a HIP device, and
+    ``--stage N`` deselects the stage-parametrised items of the other stages."""
+    if not torch.cuda.is_available():
+        no_device = pytest.mark.skip(reason="no HIP device (torch.cuda.is_available() is False)")
+        for item in items:
+            if item.get_closest_marker("gpu") is not None:
+                item.add_marker(no_device)
+    option = config.getoption("--stage")
+    if option in (None, "all"):
+        return
+    stage = int(option)
+    dropped = [it for it in items if _stage_of(it) not in (None, stage)]
+    if dropped:
+        config.hook.pytest_deselected(items=dropped)
+        items[:] = [it for it in items if _stage_of(it) in (None, stage)]
 
 
 # (B, H, N, D) shapes for the GPU parity tests: the reference's GPU_SHAPES

@@ -150,3 +150,26 @@ def test_launch_honours_the_callers_stream():
     assert rc == capi.HIP_SUCCESS
     s.synchronize()
     assert torch.equal(o, o_ref)
+
+
+def test_forced_height_alone_is_valid_on_any_grid():
+    """A forced stage-5 height without a forced width takes a built width for that height: on
+    B1 H1 N4096 D64 the automatic width is 128 and (256, 128) is not built, so BR = 256 alone runs
+    with the widest built width for that height (64). Before, the pair was refused."""
+    gen = torch.Generator().manual_seed(8)
+    q, k, v = (torch.randn(1, 1, 4096, 64, generator=gen).to("cuda", torch.float16)
+               for _ in range(3))
+    from oracle.oracle import math_reference_rows
+
+    lib = capi.load()
+    lib.fa_set_debug_overrides(256, 0)
+    try:
+        rc, o, lse = run(5, q, k, v, False, 0.125)
+    finally:
+        lib.fa_set_debug_overrides(0, 0)
+    assert rc == capi.HIP_SUCCESS, capi.error_string(rc)
+    torch.cuda.synchronize()
+    rows = np.r_[0:64, 2000:2064, 4032:4096]
+    o64, l64 = math_reference_rows(q, k, v, 0, 0, rows, is_causal=False, scale=0.125)
+    assert_close_tol(o[0, 0, rows], o64, *O_TOL[torch.float16])
+    assert_close_tol(lse[0, 0, rows], l64, LSE_ATOL, 0.0, what="LSE")
