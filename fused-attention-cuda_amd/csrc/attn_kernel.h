@@ -5,8 +5,7 @@
 //                               v_mfma_f32_32x32x2_f32, so no operand is rounded below fp32
 //                               (fp32 or fp16 I/O, ref:src/stage3_fused.cu:142-160). K/V tiles are
 //                               double-buffered in LDS with register-staged prefetch.
-// The 16-bit matrix-core stages (4 and 5) live in attn_mfma16.h. The template below still carries
-// its 16-bit operand paths (kHalf); only the fp32-operand instantiation is built.
+// The 16-bit matrix-core stages (4 and 5) live in attn_mfma16.h.
 //
 // Algorithm (FlashAttention-2 loop order, the reference's recurrence ref:include/fa/softmax_math.cuh):
 // a workgroup owns BR = 32*WAVES query rows of one (b, h); each wave owns 32 rows for the whole
@@ -24,9 +23,8 @@
 // already in the B-operand layout of the second product O^T = V^T P^T (lane l supplies column
 // n = l % 32 = its row; its 8 k-slots are 8 of its own keys). P never leaves registers -- the
 // smem round trips the reference's WMMA kernels need (ref:src/stage5_tuned.cu:63-76) do not exist.
-// The price is that V must be read "transposed" (8 keys of one head-dim column per lane): V^T is
-// therefore what the tile loader writes to LDS, with the keys of each 16-key group permuted
-// (0-3, 8-11, 4-7, 12-15) so every PV operand is one 16-byte LDS read.
+// The price is that V must be read "transposed" (keys of one head-dim column per lane): V^T is
+// therefore what the tile loader writes to LDS, so every PV operand is one 16-byte LDS read.
 //
 // LDS layout (per buffer): Ks[BC][D + pad] row-major (A operand of S^T: lane reads 16 contiguous
 // bytes of key row l % 32), then Vt[D][BC + pad]. pad = 16 bytes: rows shift by 4 banks, so the
@@ -54,96 +52,34 @@ namespace kern {
 using ::fa::KArgs;
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kNumXcd = 8;
 constexpr float kLn2 = 0.69314718055994531f;
-// Lazy rescaling threshold, in exp2 units: probabilities may reach 2^8 before m is moved. bf16
-// uses 0 (exact running max): with 8 significant bits the largest probability must stay exactly
-// 1.0, or its own rounding (2^-9 relative) dominates the error of concentrated rows.
-template <typename Tc>
-constexpr float lazy_log2() {
-  return __is_same(Tc, __bf16) ? 0.0f : 8.0f;
-}
+// Lazy rescaling threshold, in exp2 units: probabilities may reach 2^8 before m is moved.
+constexpr float kLazyLog2 = 8.0f;
 
 // 2^x on the transcendental unit (v_exp_f32). exp2(-inf) = 0, which the masking relies on.
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 // log2(x) on the transcendental unit (v_log_f32).
 __device__ __forceinline__ float log2_hw(float x) { return __builtin_amdgcn_logf(x); }
 
-// ---- element conversions -----------------------------------------------------------------------
-template <typename T>
-__device__ __forceinline__ float to_f32(T x) {
-  return static_cast<float>(x);
-}
-
-// 8 fp32 probabilities -> one 16-byte MFMA operand of 8 fp16/bf16 (round to nearest even).
-template <typename T>
-__device__ __forceinline__ u32x4 pack8(float p0, float p1, float p2, float p3, float p4, float p5,
-                                       float p6, float p7) {
-  if constexpr (sizeof(T) == 2 && __is_same(T, _Float16)) {
-    f16x8 h = {(_Float16)p0, (_Float16)p1, (_Float16)p2, (_Float16)p3,
-               (_Float16)p4, (_Float16)p5, (_Float16)p6, (_Float16)p7};
-    return __builtin_bit_cast(u32x4, h);
-  } else {
-    bf16x8 h = {(__bf16)p0, (__bf16)p1, (__bf16)p2, (__bf16)p3,
-                (__bf16)p4, (__bf16)p5, (__bf16)p6, (__bf16)p7};
-    return __builtin_bit_cast(u32x4, h);
-  }
-}
-
-// acc + sum of the 8 fp16 values packed in v, as 4 v_dot2c_f32_f16 against (1, 1). The pairs are
-// taken with shufflevector from one whole-vector bit_cast: a bit_cast of a vector element chosen
-// by a loop index is lowered to element 0 by this compiler.
-__device__ __forceinline__ float dot2_ones_f16(u32x4 v, float acc) {
-  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
-  const f16x8 h = __builtin_bit_cast(f16x8, v);
-  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 0, 1), one, acc, false);
-  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 2, 3), one, acc, false);
-  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 4, 5), one, acc, false);
-  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 6, 7), one, acc, false);
-  return acc;
-}
-
-// 32x32x16 MFMA on 16-bit operands (8 elements per lane in a/b), fp32 accumulate.
-template <typename T>
-__device__ __forceinline__ f32x16 mma16(u32x4 a, u32x4 b, f32x16 c) {
-  if constexpr (__is_same(T, _Float16)) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-}
-
 // 32x32x2 MFMA on fp32 operands (one element per lane in a/b).
 __device__ __forceinline__ f32x16 mma32(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-// Position of key kk (0..15) inside its 16-key group in the V^T LDS row: keys 0-3, 8-11, 4-7,
-// 12-15 become positions 0-15, so lane half g of the PV operand reads positions 8g..8g+7, which
-// are exactly the keys 8(i/4) + 4g + i%4 (i = 0..7) its probability registers hold.
-__device__ __forceinline__ int vt_pos16(int kk) {
-  return 8 * ((kk >> 2) & 1) + 4 * (kk >> 3) + (kk & 3);
-}
-
-// Tio: element type in HBM (q/k/v/o). Tc: operand type in LDS / MFMA (== Tio for the matrix-core
-// stages; float for the fp32 rung). WAVES: 32-row query groups per workgroup (BR = 32*WAVES).
-// BC: keys per K/V tile. PREFETCH: double-buffered LDS + register-staged next-tile loads.
-template <typename Tio, typename Tc, int D_, int WAVES, int BC_, bool PREFETCH>
+// Tio: element type in HBM (q/k/v/o: fp32 or fp16); LDS and the MFMA operands are fp32 (Tc).
+// WAVES: 32-row query groups per workgroup (BR = 32*WAVES). BC: keys per K/V tile. PREFETCH:
+// double-buffered LDS + register-staged next-tile loads.
+template <typename Tio, int D_, int WAVES, int BC_, bool PREFETCH>
 struct Attn {
+  using Tc = float;
   static constexpr int D = D_;
   static constexpr int BC = BC_;
-  static constexpr bool kHalf = sizeof(Tc) == 2;
   static constexpr int kThreads = 64 * WAVES;
   static constexpr int kBr = 32 * WAVES;
   static constexpr int kPad = 16 / static_cast<int>(sizeof(Tc));
@@ -163,14 +99,14 @@ struct Attn {
   static constexpr int kVChunks = (BC / 4) * kRowVecs;       // 4 keys x one vector per chunk
   static constexpr int kNK = (kKChunks + kThreads - 1) / kThreads;
   static constexpr int kNV = (kVChunks + kThreads - 1) / kThreads;
-  // Per-lane Q operand storage: half path D/16 vectors of 8; fp32 path D/2 floats as D/8 x 4.
-  static constexpr int kQVecs = kHalf ? D / 16 : D / 8;
+  // Per-lane Q operand storage: D/2 floats as D/8 vectors of 4.
+  static constexpr int kQVecs = D / 8;
 
   static_assert(BC % 32 == 0 && BC >= 32 && BC <= 128, "BC must be 32, 64 or 128");
   static_assert(D == 64 || D == 128, "D must be 64 or 128");
   static_assert(WAVES >= 1 && WAVES <= 8, "1..8 waves");
   static_assert(kLdsBytes <= 160 * 1024, "gfx950 LDS is 160 KiB per workgroup");
-  static_assert(!kHalf || __is_same(Tio, Tc), "16-bit operands are the I/O type itself");
+  static_assert(__is_same(Tio, float) || __is_same(Tio, _Float16), "fp32 or fp16 I/O");
 
   struct Staging {
     u32x4 kv[kNK];
@@ -235,20 +171,7 @@ struct Attn {
       if ((kVChunks % kThreads == 0) || c < kVChunks) {
         const int key0 = 4 * (c / kRowVecs);  // first of the 4 keys (tile-local)
         const int d0 = (c % kRowVecs) * kVec;
-        if constexpr (kHalf) {
-          // 4 keys x 8 head-dim values -> 8 rows of V^T, 4 keys (8 bytes) each.
-          const int pos = 16 * (key0 >> 4) + vt_pos16(key0 & 15);
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-              const uint32_t sel = e ? 0x07060302u : 0x05040100u;
-              const uint32_t lo = __builtin_amdgcn_perm(st.vv[i][1][w], st.vv[i][0][w], sel);
-              const uint32_t hi = __builtin_amdgcn_perm(st.vv[i][3][w], st.vv[i][2][w], sel);
-              *reinterpret_cast<u32x2*>(Vt + (d0 + 2 * w + e) * kLdV + pos) = u32x2{lo, hi};
-            }
-          }
-        } else if constexpr (__is_same(Tio, float)) {
+        if constexpr (__is_same(Tio, float)) {
           // 4 keys x 4 head-dim fp32 values -> 4 rows of V^T (natural key order), 16 bytes each.
           const f32x4 r0 = __builtin_bit_cast(f32x4, st.vv[i][0]);
           const f32x4 r1 = __builtin_bit_cast(f32x4, st.vv[i][1]);
@@ -278,8 +201,7 @@ struct Attn {
   // Per-wave running state: Q operand, O^T accumulator, row max (raw units) and partial row sum
   // (this lane's half of the row's keys; the two halves are added in the epilogue).
   struct WaveState {
-    u32x4 qh[kHalf ? kQVecs : 1];
-    f32x4 qf[kHalf ? 1 : kQVecs];
+    f32x4 qf[kQVecs];
     f32x16 o[kDB];
     float m;   // running row max, raw score units (may lag the true max: lazy rescaling)
     float mc;  // m * c with the -inf guard applied (0 while m == -inf)
@@ -287,26 +209,17 @@ struct Attn {
   };
 
   __device__ static void load_q(WaveState& ws, const Tio* qb, int row, int qsn, bool valid, int g) {
-    if constexpr (kHalf) {
+    // fp32 MFMA k-slot mapping: lane half g covers head-dim [g*D/2, (g+1)*D/2).
+    const Tio* src = qb + row * qsn + g * (D / 2);
 #pragma unroll
-      for (int s = 0; s < kQVecs; ++s) {
-        ws.qh[s] = valid ? *reinterpret_cast<const u32x4*>(qb + row * qsn +
-                                                           16 * s + 8 * g)
-                         : u32x4{0u, 0u, 0u, 0u};
-      }
-    } else {
-      // fp32 MFMA k-slot mapping: lane half g covers head-dim [g*D/2, (g+1)*D/2).
-      const Tio* src = qb + row * qsn + g * (D / 2);
-#pragma unroll
-      for (int j = 0; j < kQVecs; ++j) {
-        if (!valid) {
-          ws.qf[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        } else if constexpr (__is_same(Tio, float)) {
-          ws.qf[j] = *reinterpret_cast<const f32x4*>(src + 4 * j);
-        } else {
-          const f16x4 h = *reinterpret_cast<const f16x4*>(src + 4 * j);
-          ws.qf[j] = f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
-        }
+    for (int j = 0; j < kQVecs; ++j) {
+      if (!valid) {
+        ws.qf[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      } else if constexpr (__is_same(Tio, float)) {
+        ws.qf[j] = *reinterpret_cast<const f32x4*>(src + 4 * j);
+      } else {
+        const f16x4 h = *reinterpret_cast<const f16x4*>(src + 4 * j);
+        ws.qf[j] = f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
       }
     }
   }
@@ -326,19 +239,11 @@ struct Attn {
       if (kb < nvalid) {
         f32x16 acc = {};
         const Tc* krow = Ks + (32 * kb + r32) * kLdK;
-        if constexpr (kHalf) {
 #pragma unroll
-          for (int st = 0; st < D / 16; ++st) {
-            const u32x4 a = *reinterpret_cast<const u32x4*>(krow + 16 * st + 8 * g);
-            acc = mma16<Tc>(a, ws.qh[st], acc);
-          }
-        } else {
+        for (int j = 0; j < kQVecs; ++j) {
+          const f32x4 a = *reinterpret_cast<const f32x4*>(krow + g * (D / 2) + 4 * j);
 #pragma unroll
-          for (int j = 0; j < kQVecs; ++j) {
-            const f32x4 a = *reinterpret_cast<const f32x4*>(krow + g * (D / 2) + 4 * j);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc = mma32(a[e], ws.qf[j][e], acc);
-          }
+          for (int e = 0; e < 4; ++e) acc = mma32(a[e], ws.qf[j][e], acc);
         }
         s[kb] = acc;
       }
@@ -370,9 +275,9 @@ struct Attn {
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     // The reference recurrence moves m to the row max on every tile and rescales acc and l by
     // alpha = exp2((m_old - m_new) c). Here m moves only when some row of the wave sees a max
-    // more than lazy_log2<Tc>() (exp2 units) above its current m; otherwise p = exp2(s c - m c)
-    // stays <= 2^lazy_log2 and nothing is rescaled. acc, l and lse are all taken relative to the same m,
-    // so the function is unchanged, and p stays far inside the fp16/bf16/fp32 range. The decision
+    // more than kLazyLog2 (exp2 units) above its current m; otherwise p = exp2(s c - m c)
+    // stays <= 2^kLazyLog2 and nothing is rescaled. acc, l and lse are all taken relative to the same m,
+    // so the function is unchanged, and p stays far inside the fp32 range. The decision
     // is one ballot per tile (wave-uniform), so a skipped rescale costs a scalar branch.
     if (__builtin_amdgcn_ballot_w64(mx > ws.m + lazy_raw) != 0) {
       const float m_new = fmaxf(ws.m, mx);
@@ -398,57 +303,16 @@ struct Attn {
 #pragma unroll
     for (int kb = 0; kb < kKB; ++kb) {
       if (kb < nvalid) {
-        if constexpr (kHalf) {
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            float p[8];
+        for (int r = 0; r < 16; ++r) rs += s[kb][r];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) p[i] = s[kb][8 * h + i];
-            const u32x4 pf = pack8<Tc>(p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]);
-            u32x4 a[kDB];
+        for (int j = 0; j < 4; ++j) {
 #pragma unroll
-            for (int db = 0; db < kDB; ++db) {
-              a[db] = *reinterpret_cast<const u32x4*>(Vt + (32 * db + r32) * kLdV + 32 * kb +
-                                                      16 * h + 8 * g);
-              ws.o[db] = mma16<Tc>(a[db], pf, ws.o[db]);
-            }
-            if constexpr (__is_same(Tc, _Float16)) {
-              // fp16: the row sum is taken over the probabilities exactly as they enter the
-              // product (rounded to fp16), two per packed dot2 -- half the adds of fp32 sums,
-              // and numerator and denominator use the same weights.
-              rs = dot2_ones_f16(pf, rs);
-            } else {
-              // bf16 keeps 8 significant bits, so a rounded p is off by up to 2^-8 relative; the
-              // row sum stays in fp32 (the LSE must hold 1e-3). On the causal diagonal block --
-              // where the first rows of a sequence have all of their few keys -- P is applied as
-              // hi + lo (two bf16 operands, exact to ~2^-16), which removes the error that would
-              // otherwise dominate those rows; other blocks average the rounding over many keys.
+          for (int db = 0; db < kDB; ++db) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(Vt + (32 * db + r32) * kLdV +
+                                                            32 * kb + 8 * j + 4 * g);
 #pragma unroll
-              for (int i = 0; i < 8; ++i) rs += p[i];
-              if (kb == diag) {
-                float lo[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                  lo[i] = p[i] - static_cast<float>(static_cast<__bf16>(p[i]));
-                }
-                const u32x4 pl = pack8<Tc>(lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]);
-#pragma unroll
-                for (int db = 0; db < kDB; ++db) ws.o[db] = mma16<Tc>(a[db], pl, ws.o[db]);
-              }
-            }
-          }
-        } else {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) rs += s[kb][r];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-#pragma unroll
-            for (int db = 0; db < kDB; ++db) {
-              const f32x4 a = *reinterpret_cast<const f32x4*>(Vt + (32 * db + r32) * kLdV +
-                                                              32 * kb + 8 * j + 4 * g);
-#pragma unroll
-              for (int e = 0; e < 4; ++e) ws.o[db] = mma32(a[e], s[kb][4 * j + e], ws.o[db]);
-            }
+            for (int e = 0; e < 4; ++e) ws.o[db] = mma32(a[e], s[kb][4 * j + e], ws.o[db]);
           }
         }
       }
@@ -504,7 +368,7 @@ struct Attn {
     ws.mc = 0.f;
     ws.l = 0.f;
 
-    const float lazy_raw = lazy_log2<Tc>() / a.c;  // lazy-rescale threshold, raw score units
+    const float lazy_raw = kLazyLog2 / a.c;  // lazy-rescale threshold, raw score units
     Staging st;
     if constexpr (PREFETCH) {
       load_tile(st, kb, vb, 0, N, a.ksn, a.vsn, tid);
@@ -552,11 +416,9 @@ struct Attn {
         const float x2 = ws.o[db][4 * j + 2] * inv, x3 = ws.o[db][4 * j + 3] * inv;
         if constexpr (__is_same(Tio, float)) {
           *reinterpret_cast<f32x4*>(orow + d) = f32x4{x0, x1, x2, x3};
-        } else if constexpr (__is_same(Tio, _Float16)) {
+        } else {
           *reinterpret_cast<f16x4*>(orow + d) =
               f16x4{(_Float16)x0, (_Float16)x1, (_Float16)x2, (_Float16)x3};
-        } else {
-          *reinterpret_cast<bf16x4*>(orow + d) = bf16x4{(__bf16)x0, (__bf16)x1, (__bf16)x2, (__bf16)x3};
         }
       }
     }
@@ -571,13 +433,13 @@ struct Attn {
 // Kernel entry point of the fp32 rung (profiler-visible name of stage 3).
 template <typename T, int D, int WAVES, int BC>
 __global__ __launch_bounds__(64 * WAVES) void fa_s3_fused(KArgs a) {
-  Attn<T, float, D, WAVES, BC, true>::run(a);
+  Attn<T, D, WAVES, BC, true>::run(a);
 }
 
 // Host-side launch of one instantiated stage-3 variant.
 template <typename T, int D, int WAVES, int BC>
 int launch_s3(const KArgs& in, hipStream_t stream) {
-  using A = Attn<T, float, D, WAVES, BC, true>;
+  using A = Attn<T, D, WAVES, BC, true>;
   KArgs a = in;
   a.n_qtiles = (a.N + A::kBr - 1) / A::kBr;
   const long long grid = static_cast<long long>(a.n_qtiles) * a.B * a.H;

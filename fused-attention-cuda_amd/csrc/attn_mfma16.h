@@ -58,6 +58,7 @@
 #include <type_traits>
 
 #include "fa_internal.h"
+#include "tile_layout.h"
 
 namespace fa {
 namespace m16 {
@@ -166,24 +167,11 @@ struct Fa16 {
   static_assert(kChunks % 64 == 0, "a tile is a whole number of 1 KiB DMA instructions");
   static_assert(kDmaInsts % kWaves == 0, "every wave issues the same number of DMA instructions");
 
-  // LDS layout of a K/V tile: BC rows of D elements, unpadded; the 16-byte chunk c of row r
-  // lives at chunk position c ^ swz(r). The swizzles were chosen by measuring the read rate of
-  // each operand pattern on gfx950 (8 waves per CU, LDS bytes per clock):
-  //   K, 16 consecutive lanes read 16 consecutive rows (ds_read_b128): D = 64 rows are 128 bytes,
-  //     so a row pair spans the banks once and swz(r) = (r >> 1) & 7 gives the 16 lanes 16
-  //     distinct 16-byte bank groups (234 B/clk; r & 7 leaves a 2-way conflict, 147 B/clk);
-  //     D = 128 rows are 256 bytes and swz(r) = r & 15 does the same (242 against 146 B/clk).
-  //   V, one 16-lane transpose read covers 4 consecutive rows: swz(r) = 2 (r & 3) at D = 64
-  //     (129 B/clk, the best measured) and 4 (r & 3) at D = 128 (178 against 149 B/clk).
-  // Every swizzle depends on r % 32 only, so a lane's offsets inside a 32-key block are
-  // loop-invariant (blocks start at multiples of 32).
+  // LDS layout of a K/V tile (layout::swz): BC rows of D elements, unpadded, with the 16-byte
+  // chunks of each row XOR-swizzled by a function of the row chosen by measured read rate.
   template <bool IS_V>
   __device__ static int swz(int row) {
-    if constexpr (IS_V) {
-      return (D == 64 ? 2 : 4) * (row & 3);
-    } else {
-      return D == 64 ? ((row >> 1) & 7) : (row & 15);
-    }
+    return layout::swz<D, IS_V>(row);
   }
 
   // Tiles go straight from HBM into LDS with global_load_lds_dwordx4: lane i of a wave
@@ -201,9 +189,9 @@ struct Fa16 {
     Dma d;
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
-      const int pos = 64 * (wave + i * kWaves) + lane;  // chunk position in the tile
-      d.row[i] = pos / kRowChunks;
-      d.off[i] = d.row[i] * sn + 8 * ((pos % kRowChunks) ^ swz<IS_V>(d.row[i]));
+      const auto src = layout::dma_src<D, IS_V>(kWaves, wave, lane, i, sn);
+      d.row[i] = src.row;
+      d.off[i] = src.off;
     }
     return d;
   }
@@ -297,9 +285,7 @@ struct Fa16 {
   __device__ static KLane k_lane(int lane) {
     KLane k;
 #pragma unroll
-    for (int st = 0; st < D / 16; ++st) {
-      k.off[st] = (lane & 31) * D + 8 * ((2 * st + (lane >> 5)) ^ swz<false>(lane & 31));
-    }
+    for (int st = 0; st < D / 16; ++st) k.off[st] = layout::k_operand_offset<D>(lane, st);
     return k;
   }
   template <bool FULL>
@@ -440,13 +426,9 @@ struct Fa16 {
     int off[kDB];
   };
   __device__ static VLane v_lane(int lane) {
-    const int G = lane >> 4, j = (lane >> 2) & 3, q = lane & 3;
     VLane v;
 #pragma unroll
-    for (int db = 0; db < kDB; ++db) {
-      const int chunk = (4 * db + 2 * (G & 1) + (q >> 1)) ^ swz<true>(j);
-      v.off[db] = (4 * (G >> 1) + j) * D + 8 * chunk + 4 * (q & 1);
-    }
+    for (int db = 0; db < kDB; ++db) v.off[db] = layout::v_operand_offset<D>(lane, db);
     return v;
   }
   __device__ static u32x4 v_operand(const T* Vs, const VLane& vl, int kb, int h, int db) {
@@ -576,11 +558,12 @@ struct Fa16 {
     const bool wave_valid = r0 < N;
     const int row = r0 + (lane & 31);
     // Key range of the workgroup (causal stops at its last row) and of this wave. The workgroup
-    // walks key tiles [t0, n_tiles): the whole walk, or its part of a split walk.
-    const int kv_end = a.causal ? min(N, i0 + kBr) : N;
-    const int n_walk = (kv_end + BC - 1) / BC;
-    const int t0 = __builtin_amdgcn_readfirstlane(fdiv(part * n_walk, a.fd_splits));
-    const int n_tiles = __builtin_amdgcn_readfirstlane(fdiv((part + 1) * n_walk, a.fd_splits));
+    // walks key tiles [t0, n_tiles): the whole walk, or its part of a split walk; steps before
+    // n_steady take the steady body (layout::plan_walk).
+    const layout::Walk walk = layout::plan_walk(N, BC, kBr, qt, a.causal != 0, part,
+                                                [&](int x) { return fdiv(x, a.fd_splits); });
+    const int t0 = __builtin_amdgcn_readfirstlane(walk.t0);
+    const int n_tiles = __builtin_amdgcn_readfirstlane(walk.n_tiles);
     const int wave_end = wave_valid ? (a.causal ? min(N, r0 + 32) : N) : 0;
     const int kbase = ks * BCW;  // this wave's keys inside every tile
     const float c = a.c;
@@ -695,10 +678,7 @@ struct Fa16 {
       // carry the causal diagonal: the steady step only computes its scores, unmasked, and the
       // partial step that exponentiates them applies the mask and the per-wave block counts.
       // Steady steps are t in [t0, n_steady).
-      const int n_full = (a.causal ? i0 : N) / BC;
-      const int n_steady = n_full >= n_tiles
-                               ? n_tiles
-                               : max(t0, min(min(n_tiles - 1, n_full), N / BC - 2));
+      const int n_steady = __builtin_amdgcn_readfirstlane(walk.n_steady);
       // Unrolled by two so the S(t) / S(t+1) register sets swap roles without copies; the steady
       // loop and the tail loop get independent register assignments.
       int t = t0;

@@ -1,0 +1,103 @@
+// tile_layout.h -- the integer layout of the stage-4/5 kernels' K/V tiles: which global element
+// every lane of every LDS-DMA instruction copies, where a tile lives in LDS, which LDS bytes each
+// MFMA operand read touches, and which key tiles a workgroup walks and loads.
+//
+// Pure integer functions with no HIP intrinsics, compiled for the device by attn_mfma16.h and for
+// the host by tests/address_model.cpp, which replays every load of every workgroup on the CPU and
+// checks that each global read stays inside its tensor and each LDS access inside its buffer (the
+// role of the reference's compute-sanitizer memcheck run, ref:scripts/gpu_run.sh:157-181).
+#pragma once
+
+#if defined(__HIPCC__) || defined(__HIP__)
+#define FA_HD __host__ __device__
+#else
+#define FA_HD
+#endif
+
+namespace fa {
+namespace layout {
+
+// LDS layout of a K/V tile: BC rows of D 16-bit elements, unpadded; the 16-byte chunk c of row r
+// lives at chunk position c ^ swz(r). The swizzles were chosen by the measured read rate of each
+// operand pattern on gfx950: K rows are read 16 consecutive rows per 16 lanes (ds_read_b128), so
+// D = 64 rows (128 bytes) pair up, (r >> 1) & 7, and D = 128 rows use r & 15; V is read through
+// the transpose path 4 consecutive rows per 16 lanes, 2 (r & 3) at D = 64 and 4 (r & 3) at
+// D = 128. Every swizzle depends on r % 32 only, so a lane's offsets inside a 32-key block are
+// loop-invariant.
+template <int D, bool IS_V>
+FA_HD constexpr int swz(int row) {
+  if constexpr (IS_V) {
+    return (D == 64 ? 2 : 4) * (row & 3);
+  } else {
+    return D == 64 ? ((row >> 1) & 7) : (row & 15);
+  }
+}
+
+// LDS-DMA: instruction j of a tile covers chunk positions [64 j, 64 j + 64) (1 KiB) and goes to
+// wave j % waves; lane l writes position 64 j + l, so it copies the global chunk whose swizzled
+// position that is. Its source relative to the tile's first key: tile-local row `row` and element
+// offset `off` = row * sn + 8 * (its chunk in the row) for a row stride of sn elements.
+template <int D, bool IS_V>
+struct DmaSrc {
+  int row;
+  int off;
+};
+template <int D, bool IS_V>
+FA_HD inline DmaSrc<D, IS_V> dma_src(int waves, int wave, int lane, int i, int sn) {
+  constexpr int kRowChunks = D / 8;
+  const int pos = 64 * (wave + i * waves) + lane;  // chunk position in the tile
+  const int row = pos / kRowChunks;
+  return DmaSrc<D, IS_V>{row, row * sn + 8 * ((pos % kRowChunks) ^ swz<D, IS_V>(row))};
+}
+
+// K operand of S^T = K Q^T, head-dim step st: lane l reads key row l % 32 of a 32-key block,
+// chunk 2 st + l / 32 (head-dim 16 st + 8 (l / 32)); element offset inside the block.
+template <int D>
+FA_HD constexpr int k_operand_offset(int lane, int st) {
+  return (lane & 31) * D + 8 * ((2 * st + (lane >> 5)) ^ swz<D, false>(lane & 31));
+}
+
+// V^T operand through the transpose read, head-dim block db: lane l = 16 G + 4 j + q addresses key
+// row 4 (G / 2) + j of a 16-key group (and 8 rows further for the second read) at head-dim
+// 32 db + 16 (G % 2) + 4 q; element offset inside the group.
+template <int D>
+FA_HD constexpr int v_operand_offset(int lane, int db) {
+  const int G = lane >> 4, j = (lane >> 2) & 3, q = lane & 3;
+  const int chunk = (4 * db + 2 * (G & 1) + (q >> 1)) ^ swz<D, true>(j);
+  return (4 * (G >> 1) + j) * D + 8 * chunk + 4 * (q & 1);
+}
+
+// The key tiles one stage-5 workgroup walks: [t0, n_tiles) of BC keys (its part of the query
+// tile's walk when the walk is split into `splits` parts), and n_steady: steps t in
+// [t0, n_steady) take the branch-free steady body, whose loads (K(t+2), V(t+1), clamped to the last
+// tile of the walk) are whole tiles inside the tensor. The rule, in the kernel's words: when every
+// tile of the walk is full, all of them take the steady step; otherwise step t needs tile t full
+// and free of the causal diagonal, t + 1 inside the walk, and t + 3 <= N / BC.
+struct Walk {
+  int t0;
+  int n_tiles;
+  int n_steady;
+};
+// div_splits(x) must return x / splits (the kernel passes its multiply-shift division).
+template <typename DivSplits>
+FA_HD inline Walk plan_walk(int N, int BC, int BR, int qt, bool causal, int part,
+                            DivSplits div_splits) {
+  const int i0 = qt * BR;
+  const int kv_end = causal ? (N < i0 + BR ? N : i0 + BR) : N;
+  const int n_walk = (kv_end + BC - 1) / BC;
+  Walk w;
+  w.t0 = div_splits(part * n_walk);
+  w.n_tiles = div_splits((part + 1) * n_walk);
+  const int n_full = (causal ? i0 : N) / BC;
+  if (n_full >= w.n_tiles) {
+    w.n_steady = w.n_tiles;
+  } else {
+    int s = w.n_tiles - 1 < n_full ? w.n_tiles - 1 : n_full;
+    s = s < N / BC - 2 ? s : N / BC - 2;
+    w.n_steady = s > w.t0 ? s : w.t0;
+  }
+  return w;
+}
+
+}  // namespace layout
+}  // namespace fa

@@ -342,3 +342,22 @@ def test_c_oracle_matches_live_reference(b, h, hkv, n, d, causal, c_oracle):
                                      threads=3)
     assert np.array_equal(o_h, o_r.reshape(b * h, n, d)[1:])
     assert np.array_equal(lse_h, lse_r.reshape(b * h, n)[1:])
+
+
+def test_reference_ctest_passes():
+    """The reference's own oracle test binary (ref:src/reference/test_cpu_reference.cpp, its ctest
+    target ref:CMakeLists.txt:33-37), built from the reference's sources by ``make -C oracle ref``:
+    it must pass here too, so the oracle the golden vectors came from is the tested one."""
+    import subprocess
+
+    root = Path(__file__).resolve().parents[1]
+    exe = root / "oracle" / "_ref" / "test_cpu_reference"
+    if Path("/root/reference/src/reference/test_cpu_reference.cpp").exists():
+        cmd = ["make", "-s", "-C", str(root / "oracle"), "ref-check"]  # builds, then runs it
+    elif exe.exists():
+        cmd = [str(exe)]  # a tree without the reference sources: the binary built earlier
+    else:
+        pytest.skip("the reference sources are absent and oracle/_ref was not built")
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-2000:]
+    assert "PASS" in res.stdout, res.stdout[-2000:]
