@@ -7,7 +7,11 @@
 //   * 4 rotating input sets (fewer only when memory is short; notes say `sets=<n>`), uniform in
 //     [-1, 1) from a counter-based hash on the device, one seed per tensor and set;
 //   * a 1 GiB buffer is cleared before EVERY timed launch, outside the event pair: 256 MB, the
-//     reference's size, no longer exceeds the L2 plus the 256 MB Infinity Cache of an MI355X;
+//     reference's size, no longer exceeds the L2 plus the 256 MB Infinity Cache of an MI355X.
+//     `--flush 0` drops it (notes say `flush=none`): launches then run back to back over the
+//     rotating sets, the way a caller's loop issues them, which is how the tile-rule captures
+//     of profile.sh compare tiles (the write-back of the flushed lines otherwise overlaps the
+//     next launch and stretches it: C128 52 us after the flush, 42 us back to back);
 //   * one hipEvent pair per launch, one hipDeviceSynchronize after the loop;
 //   * iterations: at least --iters (100) and at least 500 ms of timed work, sized from three
 //     launches after the warmup;
@@ -131,6 +135,7 @@ struct Options {
   int check_rows = 64;
   int hkv = 0;
   float scale = 0.f;
+  int flush = 1;  // 1 GiB flush before every launch (the reference's protocol); 0: back to back
   bool list = false;
   bool smoke = false;
 };
@@ -139,7 +144,7 @@ void usage(FILE* f) {
   std::fprintf(f,
                "fa_bench --stage N [--cfg C64|C128|B2_H8_N2048_D64] [--dtype fp32|fp16|bf16]\n"
                "         [--causal 0|1] [--iters 100] [--warmup 10] [--out path.csv]\n"
-               "         [--commit sha] [--check-rows 64] [--hkv H] [--scale s]\n"
+               "         [--commit sha] [--check-rows 64] [--hkv H] [--scale s] [--flush 1|0]\n"
                "fa_bench --smoke [--stage N]   # one small launch + check, no CSV row\n"
                "fa_bench --list                # stage x dtype x D support on this GPU\n");
 }
@@ -178,6 +183,7 @@ int parse_args(int argc, char** argv, Options* o) {
       else if (a == "--check-rows") ok = parse_int(v, &o->check_rows);
       else if (a == "--hkv") ok = parse_int(v, &o->hkv);
       else if (a == "--scale") o->scale = std::strtof(v, nullptr);
+      else if (a == "--flush") ok = parse_int(v, &o->flush) && (o->flush == 0 || o->flush == 1);
       else ok = false;
       if (!ok) return kUsage;
     }
@@ -455,7 +461,8 @@ int run(const Options& opt, const DeviceInfo& dev, hipStream_t stream) {
   const std::size_t lse_bytes = static_cast<std::size_t>(p.B) * p.H * p.N * sizeof(float);
   const std::size_t ws_bytes = fa_workspace_bytes(opt.stage, dt, &p);
   const std::size_t set_bytes = q_bytes + 2 * kv_bytes;
-  const std::size_t fixed = q_bytes + lse_bytes + ws_bytes + kFlushBytes;
+  const std::size_t flush_bytes = opt.flush ? kFlushBytes : 0;
+  const std::size_t fixed = q_bytes + lse_bytes + ws_bytes + flush_bytes;
   // Rotating input sets: as many as fit (at most kMaxSets) in 90 % of the free memory after the
   // buffers every launch shares (O, LSE, workspace, the flush buffer).
   const std::size_t usable = dev.free / 10 * 9;
@@ -486,7 +493,7 @@ int run(const Options& opt, const DeviceInfo& dev, hipStream_t stream) {
   HIP_OK(hipMalloc(&o, q_bytes));
   HIP_OK(hipMalloc(reinterpret_cast<void**>(&lse), lse_bytes));
   if (ws_bytes > 0) HIP_OK(hipMalloc(&ws, ws_bytes));
-  HIP_OK(hipMalloc(&flush, kFlushBytes));
+  if (flush_bytes > 0) HIP_OK(hipMalloc(&flush, flush_bytes));
   auto launch = [&](int s) {
     return fa_forward(opt.stage, dt, q[s], k[s], v[s], o, lse, ws, &p, stream);
   };
@@ -516,7 +523,7 @@ int run(const Options& opt, const DeviceInfo& dev, hipStream_t stream) {
   // Timed loop: warmup, then (unless --iters was given) size the count from three launches.
   const int warmup = opt.smoke ? 1 : opt.warmup;
   for (int w = 0; w < warmup; ++w) {
-    HIP_OK(hipMemsetAsync(flush, 0, kFlushBytes, stream));
+    if (flush_bytes > 0) HIP_OK(hipMemsetAsync(flush, 0, flush_bytes, stream));
     if ((err = launch(w % nsets)) != hipSuccess) break;
   }
   int iters = opt.smoke ? 3 : opt.iters;
@@ -536,7 +543,7 @@ int run(const Options& opt, const DeviceInfo& dev, hipStream_t stream) {
   std::vector<hipEvent_t> ev(2 * static_cast<std::size_t>(iters));
   for (hipEvent_t& e : ev) HIP_OK(hipEventCreate(&e));
   for (int i = 0; i < iters && err == hipSuccess; ++i) {
-    HIP_OK(hipMemsetAsync(flush, 0, kFlushBytes, stream));  // cache eviction, untimed
+    if (flush_bytes > 0) HIP_OK(hipMemsetAsync(flush, 0, flush_bytes, stream));  // untimed eviction
     HIP_OK(hipEventRecord(ev[2 * i], stream));
     err = launch(i % nsets);
     HIP_OK(hipEventRecord(ev[2 * i + 1], stream));
@@ -557,7 +564,7 @@ int run(const Options& opt, const DeviceInfo& dev, hipStream_t stream) {
   notes.push_back("clock=unlocked");
   notes.push_back("iters=" + std::to_string(iters));
   notes.push_back("warmup=" + std::to_string(warmup));
-  notes.push_back("flush=1GiB");
+  notes.push_back(flush_bytes > 0 ? "flush=1GiB" : "flush=none");
   if (p10 > 0 && p90 / p10 >= kNoiseRatio) notes.push_back("noisy");
   const double flops = 4.0 * p.B * p.H * static_cast<double>(p.N) * p.N * p.D * (p.causal ? 0.5 : 1.0);
   const double bytes = 2.0 * q_bytes + 2.0 * kv_bytes + lse_bytes;
@@ -583,7 +590,7 @@ int run(const Options& opt, const DeviceInfo& dev, hipStream_t stream) {
   }
   HIP_OK(hipFree(o));
   HIP_OK(hipFree(lse));
-  HIP_OK(hipFree(flush));
+  if (flush != nullptr) HIP_OK(hipFree(flush));
   if (ws != nullptr) HIP_OK(hipFree(ws));
   return ok ? kOk : kError;
 }

@@ -819,6 +819,9 @@ __global__ __launch_bounds__(64 * RG * KS) void fa_s4_mfma(KArgs a) {
 // O = sum_s w_s O_s / sum_s w_s and LSE = L* + ln sum_s w_s (the log-sum-exp merge of partial
 // softmax states, ref:include/fa/softmax_math.cuh:65-68; empty parts carry LSE_s = -inf and weigh
 // nothing). One thread per four head-dim elements of a row; fp32 throughout, one rounding to T.
+// Every part's LSE and partial O are loaded before the first is used (the part loop is unrolled
+// to kMaxSplitParts and predicated on n_splits), so the kernel waits for memory once, not once
+// per part and pass.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void fa_s5_combine(KArgs a) {
   constexpr int kTpr = D / 4;  // threads per row
@@ -829,8 +832,20 @@ __global__ __launch_bounds__(256) void fa_s5_combine(KArgs a) {
   if (r >= rows) return;
   const int d = 4 * (threadIdx.x % kTpr);
   const int S = a.n_splits;
+  float ls[kMaxSplitParts];
+  float4 po[kMaxSplitParts];
+#pragma unroll
+  for (int sp = 0; sp < kMaxSplitParts; ++sp) {
+    if (sp < S) {
+      ls[sp] = a.lse_part[sp * rows + r];
+      po[sp] = *reinterpret_cast<const float4*>(a.o_part + (sp * rows + r) * D + d);
+    }
+  }
   float lmax = -__builtin_inff();
-  for (int sp = 0; sp < S; ++sp) lmax = fmaxf(lmax, a.lse_part[sp * rows + r]);
+#pragma unroll
+  for (int sp = 0; sp < kMaxSplitParts; ++sp) {
+    if (sp < S) lmax = fmaxf(lmax, ls[sp]);
+  }
   const long long bh = r / a.N;
   const int n = static_cast<int>(r - bh * a.N);
   const int b = static_cast<int>(bh / a.H);
@@ -839,14 +854,16 @@ __global__ __launch_bounds__(256) void fa_s5_combine(KArgs a) {
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   float sum = 0.f;
   if (lmax != -__builtin_inff()) {
-    for (int sp = 0; sp < S; ++sp) {
-      const float w = exp2_hw((a.lse_part[sp * rows + r] - lmax) * kLog2e);
-      const float4 v = *reinterpret_cast<const float4*>(a.o_part + (sp * rows + r) * D + d);
-      sum += w;
-      acc[0] = __builtin_fmaf(w, v.x, acc[0]);
-      acc[1] = __builtin_fmaf(w, v.y, acc[1]);
-      acc[2] = __builtin_fmaf(w, v.z, acc[2]);
-      acc[3] = __builtin_fmaf(w, v.w, acc[3]);
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplitParts; ++sp) {
+      if (sp < S) {
+        const float w = exp2_hw((ls[sp] - lmax) * kLog2e);
+        sum += w;
+        acc[0] = __builtin_fmaf(w, po[sp].x, acc[0]);
+        acc[1] = __builtin_fmaf(w, po[sp].y, acc[1]);
+        acc[2] = __builtin_fmaf(w, po[sp].z, acc[2]);
+        acc[3] = __builtin_fmaf(w, po[sp].w, acc[3]);
+      }
     }
   }
   // A row no part saw (impossible for a non-empty walk) keeps O = 0 and LSE = +inf.
@@ -866,8 +883,8 @@ int launch_combine(const KArgs& a, hipStream_t stream) {
   constexpr int kRows = 256 / (D / 4);
   const long long rows = static_cast<long long>(a.B) * a.H * a.N;
   const long long grid = (rows + kRows - 1) / kRows;
-  if (a.n_splits < 2 || a.o_part == nullptr || a.lse_part == nullptr || grid <= 0 ||
-      grid > 0x7fffffffLL) {
+  if (a.n_splits < 2 || a.n_splits > kMaxSplitParts || a.o_part == nullptr ||
+      a.lse_part == nullptr || grid <= 0 || grid > 0x7fffffffLL) {
     return static_cast<int>(hipErrorInvalidValue);
   }
   hipLaunchKernelGGL((fa_s5_combine<T, D>), dim3(static_cast<unsigned>(grid)), dim3(256), 0,

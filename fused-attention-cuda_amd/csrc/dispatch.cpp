@@ -270,17 +270,18 @@ constexpr int kDefaultBcF32 = 32;
 // grid, B * H * ceil(N / BR) workgroups, still gives every compute unit one. Every workgroup walks
 // the same key tiles whatever its height (all N keys, or up to its last row when causal), so below
 // one workgroup per CU a shorter workgroup adds CUs to the problem without lengthening the
-// longest one. Measured on MI355X, B1 H16 D128 bf16 causal: N = 512 18.1 -> 12.9 us (BR 32),
-// N = 1024 26.8 -> 21.3 us (BR 64); at N = 2048 and above BR 128 stays the fastest. Heights
-// whose (BR, BC) pair is not instantiated are passed over. Each 32-row wave computes its rows
-// with the same key split and key order at every height, so the choice does not change results.
+// longest one. Heights whose (BR, BC) pair is not instantiated are passed over. Each 32-row wave
+// computes its rows with the same key split and key order at every height, so the choice does
+// not change results. Measured (profiles/tile_rule_short_walk_s5.md, B1 H16 D128 bf16 causal):
+// N = 512 13.5 us at BR 32 against 17.5 at BR 128, N = 1024 21.1 us at BR 64 against 26.5.
 //
 // Short key walks take BR 64 as well: when a 128-row workgroup would average fewer than 8 key
 // tiles (causal: about half of N / BC), its fixed cost (the first memory round trip, the key-split
-// merge, the epilogue) is a large share of it, and 64-row workgroups (4 waves, two per CU, no
-// shared barrier) overlap one workgroup's fixed cost with another's steps. Measured: the GPT-2
-// attention shape (B8 H12 N1024 D64 fp16 causal, 4.5 tiles on average) 43.1 -> 37.3 us, while
-// C64 (16 tiles) stays faster at BR 128 (29.3 against 30.6 us).
+// merge, the epilogue) is a large share of it, and 64-row workgroups (4 waves, two or more per
+// CU, no shared barrier) overlap one workgroup's fixed cost with another's steps. Measured
+// (profiles/tile_rule_d64_narrow_s5.md): the GPT-2 attention shape (B8 H12 N1024 D64 fp16
+// causal, 4.5 tiles on average) 32.9 us against 43.4 at BR 128, while C64 (16 tiles) stays
+// faster at BR 128 (27.4 against 27.8 us).
 // A short key walk: fewer than 8 default key tiles per 128-row workgroup on average (causal:
 // about half of N / BC).
 bool short_walk_s5(const fa_params& p) {
@@ -289,12 +290,13 @@ bool short_walk_s5(const fa_params& p) {
   return (p.causal ? tiles + 1 : 2 * tiles) < 16;  // twice the average
 }
 
-// D = 64 with 64-row workgroups and 32 keys per wave (BR 64, BC 64): about 150 VGPRs, so three
-// 4-wave workgroups share a CU instead of two and hide more of each other's fixed cost. Taken
-// for short walks, and wherever the grid holds at least three such workgroups per CU. Measured
-// (fp16, us, against BR 128 / BC 128): the GPT-2 attention shape B8 H12 N1024 causal 32.5
-// against 37.1; B8 H32 N1024 122.9 against 138.1; B8 H32 N2048 377.6 against 394.0. C64
-// (B2 H8 N2048, two per CU) stays at BR 128 / BC 128 (26.7 against 28.2).
+// D = 64 with 64-row workgroups and 32 keys per wave (BR 64, BC 64): 76 VGPRs and 32 KiB of LDS,
+// so up to five 4-wave workgroups share a CU where the default tile (104 VGPRs, 64 KiB) fits two.
+// Taken for short walks, and wherever the grid holds at least three such workgroups per CU.
+// Measured (profiles/tile_rule_d64_narrow_s5.md, fp16, us, against BR 128 / BC 128): the GPT-2
+// attention shape B8 H12 N1024 causal 32.9 against 43.4 (2.43 resident waves per busy SIMD
+// against 1.84); B8 H32 N2048 431.9 against 445.2. C64 (B2 H8 N2048, two narrow workgroups per
+// CU) stays at BR 128 / BC 128 (27.4 against 27.8).
 bool d64_narrow_s5(const fa_params& p, long long cus) {
   if (p.D != 64) return false;
   if (short_walk_s5(p)) return true;
@@ -304,13 +306,14 @@ bool d64_narrow_s5(const fa_params& p, long long cus) {
 
 // D = 128 with one key split of 32 keys per 32-row wave (BC 32; BR 128 is a 4-wave workgroup
 // with no key-split merge). Taken when the grid holds at least two BR-128 workgroups per CU:
-// two 4-wave workgroups then share each CU without a common barrier. Measured (fp16, us,
-// against BC 64): B8 H32 N1024 192.1 against 231.2, N2048 587.8 against 705.4, N1024 causal
-// 136.7 against 177.3, N4096 causal 1223 against 1394. C128 (B2 H8 N2048, one workgroup per CU)
-// stays at BC 64 (42.1 against 48.9). Causal long walks need four per CU: with two, the two
-// workgroups resident on a CU are tiles of equal length from two heads, so the CUs holding the
-// longest tiles hold two of them (B1 H16 N4096 causal: 123.0 against 94.3 us), where the
-// 8-wave kernel hands tiles to CUs as they free up.
+// two 4-wave workgroups then share each CU without a common barrier. Measured
+// (profiles/tile_rule_d128_narrow_s5.md, us, against BC 64): B8 H32 N1024 fp16 200.0 against
+// 242.3; LONG (B1 H16 N8192 bf16 causal) 355.5 against 405.8. C128 (B2 H8 N2048, one workgroup
+// per CU, which would leave one wave per SIMD) stays at BC 64 (43.0 against 51.0; causal 37.1
+// against 47.6). Causal long walks need four per CU: with two, the two workgroups resident on a
+// CU are tiles of equal length from two heads, so the CUs holding the longest tiles hold two of
+// them (B1 H16 N4096 bf16 causal: 115.1 at BC 64 against 135.9), where the 8-wave kernel hands
+// tiles to CUs as they free up.
 bool d128_narrow_s5(const fa_params& p, long long cus) {
   if (p.D != 128) return false;
   const long long grid128 = static_cast<long long>(p.B) * p.H * ((p.N + 127) / 128);
@@ -375,7 +378,7 @@ int width_for_forced_height(VariantList list, int D, int br, int auto_bc) {
 // at D 64 and 128, causal or not; B1 H16 at N 512-8192 causal; B8 H12 N1024 D64 causal).
 // FA_FORCE_SPLITS (test-only) forces S; fa_workspace_bytes and fa_forward must see the same
 // value.
-constexpr int kMaxSplits = 16;
+constexpr int kMaxSplits = kMaxSplitParts;
 constexpr int kModelCus = 256;
 int s5_splits(const fa_params& p, int dtype) {
   if (const int f = env_positive_int("FA_FORCE_SPLITS")) return std::min(f, kMaxSplits);

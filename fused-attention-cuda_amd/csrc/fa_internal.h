@@ -70,12 +70,15 @@ struct KArgs {
   // n_splits parts of whole tiles, one workgroup each, and each part writes its normalised fp32
   // partial O to o_part [n_splits, B, H, N, D] and its LSE to lse_part [n_splits, B, H, N]
   // (-inf for an empty part); fa_s5_combine then writes o and lse. n_splits = 1: no split.
-  int n_splits;
+  int n_splits;  // 1 .. kMaxSplitParts
   float* o_part;
   float* lse_part;
   // Divisors of the grid decode (see FastDiv): n_qtiles, H, H / Hkv and n_splits.
   FastDiv fd_qtiles, fd_h, fd_group, fd_splits;
 };
+
+// Most parts a split key walk is cut into (fa_s5_combine holds one register set per part).
+constexpr int kMaxSplitParts = 16;
 
 // Arguments of the split-KV decode kernels (attn_decode.h). q, o: [B, H, Nq, D]; k, v:
 // [B, Hkv, Nkv, D], all dense; lse [B, H, Nq]. o_part [B, Hkv, S, R, D] and lse_part
