@@ -144,6 +144,11 @@ struct Fa16 {
   static constexpr int kVElems = BC * D;  // one V buffer
   static constexpr int kBufs = PIPE ? 2 : 1;
   static constexpr size_t kTileBytes = static_cast<size_t>(kBufs) * (kKElems + kVElems) * 2;
+  // Stage 5 stages the workgroup's Q tile through LDS as well (K layout, BR rows): every prologue
+  // load is then an LDS-DMA, so the first memory round trip carries Q, K(0), V(0) and K(1) at once
+  // and the kernel waits for exactly the loads it needs (see run()).
+  static constexpr size_t kQBytes = PIPE ? static_cast<size_t>(kBr) * D * 2 : 0;
+  static constexpr int kQInsts = kBr * D / 8 / 64 / kWaves;  // Q LDS-DMA instructions per wave
   static constexpr int kKB = BCW / 32;  // 32-key blocks per wave and tile
   static constexpr int kDB = D / 32;    // 32-wide head-dim blocks of O^T
   static constexpr int kRowChunks = D / 8;         // 16-byte chunks per K/V row
@@ -154,7 +159,8 @@ struct Fa16 {
   static constexpr int kMergeFloats = (kDB * 16 + 2) * 64;
   static constexpr size_t kMergeBytes =
       KS > 1 ? static_cast<size_t>(KS - 1) * RG * kMergeFloats * sizeof(float) : 0;
-  static constexpr size_t kLdsBytes = kTileBytes > kMergeBytes ? kTileBytes : kMergeBytes;
+  static constexpr size_t kLdsBytes =
+      kTileBytes + kQBytes > kMergeBytes ? kTileBytes + kQBytes : kMergeBytes;
   // fp16 fast path: p = exp2(s c - m c) is used as long as every probability of the tile stays
   // <= 2^14 (so the fp16 operand, max 65504, cannot overflow); the check is the lane's tile row
   // sum, which bounds each of its probabilities.
@@ -166,6 +172,8 @@ struct Fa16 {
   static_assert(kLdsBytes <= 160 * 1024, "gfx950 LDS is 160 KiB per workgroup");
   static_assert(kChunks % 64 == 0, "a tile is a whole number of 1 KiB DMA instructions");
   static_assert(kDmaInsts % kWaves == 0, "every wave issues the same number of DMA instructions");
+  static_assert(kBr * D / 8 % (64 * kWaves) == 0, "the Q tile is whole DMA instructions per wave");
+  static_assert(2 * kDmaPerWave < 64, "prologue vmcnt immediates fit 6 bits");
 
   // LDS layout of a K/V tile (layout::swz): BC rows of D elements, unpadded, with the 16-byte
   // chunks of each row XOR-swizzled by a function of the row chosen by measured read rate.
@@ -237,6 +245,14 @@ struct Fa16 {
 
   // Waits until this wave's LDS-DMA loads have landed (vmcnt(0); expcnt and lgkmcnt untouched).
   __device__ static void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+  // Waits until at most n (< 64) of this wave's loads are outstanding: they complete in issue
+  // order, so every load issued before the last n has landed. vmcnt is split over bits 3:0 and
+  // 15:14 of the immediate.
+  template <int n>
+  __device__ static void wait_dma_but() {
+    static_assert(n >= 0 && n < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (n & 15) | ((n >> 4) << 14));
+  }
 
   // One 1 KiB LDS-DMA instruction from inline assembly. The compiler does not see it as a load
   // that may write LDS, so it adds no vmcnt wait of its own before later LDS reads; the caller
@@ -569,10 +585,12 @@ struct Fa16 {
     const float c = a.c;
 
     WaveState ws;
+    if constexpr (!PIPE) {
 #pragma unroll
-    for (int st = 0; st < D / 16; ++st) {
-      ws.q[st] = wave_valid ? *reinterpret_cast<const u32x4*>(qb + row * a.qsn + 16 * st + 8 * g)
-                            : u32x4{0u, 0u, 0u, 0u};
+      for (int st = 0; st < D / 16; ++st) {
+        ws.q[st] = wave_valid ? *reinterpret_cast<const u32x4*>(qb + row * a.qsn + 16 * st + 8 * g)
+                              : u32x4{0u, 0u, 0u, 0u};
+      }
     }
 #pragma unroll
     for (int db = 0; db < kDB; ++db) ws.o[db] = f32x16{};
@@ -606,15 +624,32 @@ struct Fa16 {
       // run, then applies P(t) to V(t). K is therefore staged one tile ahead of V: with u = t - t0,
       // iteration t reads K buffer (u+1)%2 and V buffer u%2 and refills K buffer u%2 with K(t+2)
       // and V buffer (u+1)%2 with V(t+1).
-      // Prologue: wait only for Q and K(t0), which QK(t0) reads; V(t0) and K(t0+1) are issued
-      // after that wait (inline-asm DMA, which the compiler does not make QK's LDS reads wait
-      // for) and land while QK(t0) runs. The full wait before the second barrier publishes them.
-      dma_tile<false>(kbuf0, kg, dk, t0 * BC, N, ksn, wave);
-      wait_dma();
-      __syncthreads();
-      dma_tile_asm<true>(vbuf0, vg, dv, t0 * BC, N, vsn, wave);
-      if (t0 + 1 < n_tiles) {
-        dma_tile_asm<false>(kbuf0 + kKElems, kg, dk, (t0 + 1) * BC, N, ksn, wave);
+      // Prologue: one memory round trip. Q (into its own LDS region, K layout), K(t0), V(t0) and
+      // K(t0+1) are all in flight at once, through inline-asm DMA: the compiler tracks none of
+      // them, so it adds no wait of its own, and the kernel waits for exactly what it reads --
+      // Q and K(t0) (issued first) before QK(t0), the rest (landing while QK(t0) runs) before the
+      // second barrier. Q rows past N read row N-1 (their waves store nothing).
+      {
+        T* const qbuf = lds + kBufs * (kKElems + kVElems);
+        const T* qtile = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
+#pragma unroll
+        for (int i = 0; i < kQInsts; ++i) {
+          const auto src = layout::dma_src<D, false>(kWaves, wave, lane, i, a.qsn);
+          const int qrow = min(i0 + src.row, N - 1);
+          dma_asm(qtile + src.off + (qrow - src.row) * a.qsn, qbuf + 512 * (wave + i * kWaves));
+        }
+        dma_tile_asm<false>(kbuf0, kg, dk, t0 * BC, N, ksn, wave);
+        dma_tile_asm<true>(vbuf0, vg, dv, t0 * BC, N, vsn, wave);
+        if (t0 + 1 < n_tiles) {
+          dma_tile_asm<false>(kbuf0 + kKElems, kg, dk, (t0 + 1) * BC, N, ksn, wave);
+          wait_dma_but<2 * kDmaPerWave>();
+        } else {
+          wait_dma_but<kDmaPerWave>();
+        }
+        __syncthreads();  // Q and K(t0) visible
+#pragma unroll
+        for (int st = 0; st < D / 16; ++st)
+          ws.q[st] = *reinterpret_cast<const u32x4*>(qbuf + 32 * rg * D + kl.off[st]);
       }
       f32x16 sa[kKB], sb[kKB];
       {

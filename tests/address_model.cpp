@@ -10,6 +10,9 @@
 //   * every LDS-DMA destination lies inside its tile buffer, and one tile's DMA writes each
 //     16-byte chunk of the buffer exactly once (no valid row is left unwritten);
 //   * every MFMA operand read (K rows, V^T transpose reads) lies inside the tile buffer;
+//   * stage 5's Q tile (BR rows in the K layout, rows past N clamped to N - 1) is read from inside
+//     its [N, D] head and written once per chunk into its LDS region, and each wave's Q register
+//     reads from that region stay inside it;
 //   * a split part's partial rows lie inside the workspace the library sizes for it.
 // Decode's split kernel (attn_decode.h) is replayed the same way: each split's keys [k_begin,
 // k_end) in 128-key tiles with the last tile clamped to the split's last key.
@@ -109,6 +112,49 @@ void check_operand_reads(const Variant& v) {
   }
 }
 
+// Stage 5's Q tile: rows [qt * BR, qt * BR + BR) of the head (row stride sn), K layout, through
+// every wave's LDS-DMA; then each wave's Q operand reads (its 32-row block).
+template <int D>
+void check_q_load(const Variant& v, int N, int sn, int qt, const std::string& c) {
+  const int waves = v.RG * v.KS;
+  const int BR = 32 * v.RG;
+  const int chunks = BR * D / 8;
+  if (chunks % (64 * waves) != 0) fail("Q tile is not whole DMA instructions per wave: " + c);
+  const int per_wave = chunks / 64 / waves;
+  const long long head_end = static_cast<long long>(N - 1) * sn + D;
+  const int i0 = qt * BR;
+  std::vector<int> written(chunks, 0);
+  for (int w = 0; w < waves; ++w) {
+    for (int i = 0; i < per_wave; ++i) {
+      for (int lane = 0; lane < 64; ++lane) {
+        const auto src = fa::layout::dma_src<D, false>(waves, w, lane, i, sn);
+        int qrow = i0 + src.row;
+        if (!g_plant_no_clamp && qrow > N - 1) qrow = N - 1;
+        const long long elem = static_cast<long long>(i0) * sn + src.off +
+                               static_cast<long long>(qrow - i0 - src.row) * sn;
+        if (elem < 0 || elem + 8 > head_end) fail("Q DMA source outside the head: " + c);
+        const int pos = 64 * (w + i * waves) + lane;
+        if (pos < 0 || pos >= chunks) fail("Q DMA destination outside the Q region: " + c);
+        ++written[pos];
+        ++g_checks;
+      }
+    }
+  }
+  for (int p = 0; p < chunks; ++p) {
+    if (written[p] != 1) fail("Q chunk " + std::to_string(p) + " written " +
+                              std::to_string(written[p]) + " times: " + c);
+  }
+  for (int rg = 0; rg < v.RG; ++rg) {
+    for (int lane = 0; lane < 64; ++lane) {
+      for (int st = 0; st < D / 16; ++st) {
+        const int e = 32 * rg * D + fa::layout::k_operand_offset<D>(lane, st);
+        if (e < 0 || e + 8 > BR * D) fail("Q operand read outside the Q region: " + c);
+        ++g_checks;
+      }
+    }
+  }
+}
+
 // The load schedule of one stage-5 (pipelined) or stage-4 (synchronous) workgroup.
 template <int D>
 void replay_workgroup(const Variant& v, int N, int sn, bool causal, int S, int part, int qt,
@@ -128,7 +174,8 @@ void replay_workgroup(const Variant& v, int N, int sn, bool causal, int S, int p
     }
     return;
   }
-  // Prologue: K(t0), V(t0), K(t0 + 1).
+  // Prologue: Q, K(t0), V(t0), K(t0 + 1).
+  check_q_load<D>(v, N, sn, qt, c + " (Q)");
   check_tile_load<D, false>(v, N, sn, walk.t0 * BC, true, c);
   check_tile_load<D, true>(v, N, sn, walk.t0 * BC, true, c);
   if (walk.t0 + 1 < walk.n_tiles) check_tile_load<D, false>(v, N, sn, (walk.t0 + 1) * BC, true, c);
