@@ -1,0 +1,179 @@
+// phase_clocks -- the per-phase cycle budget of the stage-5 kernel (fa_s5_tuned), read from the
+// kernel itself. This translation unit compiles the kernel header with FA_PHASE_CLOCKS defined, so
+// every wave records s_memtime / s_memrealtime stamps of its phases (prologue, key walk, merge and
+// epilogue) and the cycles it waits at the step barriers; the library (libfa_hip.so) is built
+// without them. The tool times K back-to-back launches over 4 rotating input sets (the same
+// kernels and tiles the library launches for the shapes below) and prints, from the last launch's
+// stamps: the launch time, the workgroups' lifetime, dispatch spread and finish spread, the mean
+// cycles of each phase, the cycles per key-tile step and the barrier wait per step, and the shader
+// clock (s_memtime cycles over s_memrealtime's 100 MHz).
+//
+//   usage: phase_clocks [C64|C128|C128_causal|all] [launches]
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#ifndef FA_PHASE_CLOCKS
+#define FA_PHASE_CLOCKS 1
+#endif
+#include "attn_mfma16.h"
+
+namespace {
+
+#define CHECK(x)                                                                          \
+  do {                                                                                    \
+    hipError_t e_ = (x);                                                                  \
+    if (e_ != hipSuccess) {                                                               \
+      std::fprintf(stderr, "phase_clocks: %s at %s:%d\n", hipGetErrorString(e_), __FILE__, \
+                   __LINE__);                                                             \
+      std::exit(1);                                                                       \
+    }                                                                                     \
+  } while (0)
+
+struct Shape {
+  const char* name;
+  int B, H, N, D, causal;
+  fa::LaunchFn fn;  // the tile the library picks for this shape (BR 128; BC 128 / 64)
+  int bc;
+};
+
+const Shape kShapes[] = {
+    {"C64", 2, 8, 2048, 64, 0, &fa::m16::launch<5, _Float16, 64, 4, 2, 64>, 128},
+    {"C128", 2, 8, 2048, 128, 0, &fa::m16::launch<5, _Float16, 128, 4, 2, 32>, 64},
+    {"C128_causal", 2, 8, 2048, 128, 1, &fa::m16::launch<5, _Float16, 128, 4, 2, 32>, 64},
+};
+
+__global__ void fill(_Float16* p, size_t n, uint32_t seed) {
+  for (size_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += gridDim.x * 256ull) {
+    uint32_t h = static_cast<uint32_t>(i) * 0x9E3779B1u ^ seed;
+    h ^= h >> 16;
+    h *= 0x85EBCA6Bu;
+    h ^= h >> 13;
+    h *= 0xC2B2AE35u;
+    h ^= h >> 16;
+    // sum of two uniforms, centred: a bell-shaped value in (-1, 1)
+    const float u = ((h & 0xFFFF) + (h >> 16)) * (1.0f / 65536.0f) - 1.0f;
+    p[i] = static_cast<_Float16>(1.7f * u);
+  }
+}
+
+void run(const Shape& s, int launches) {
+  const size_t n = static_cast<size_t>(s.B) * s.H * s.N * s.D;
+  constexpr int kSets = 4;
+  std::vector<void*> q(kSets), k(kSets), v(kSets), o(kSets);
+  std::vector<float*> lse(kSets);
+  for (int i = 0; i < kSets; ++i) {
+    for (void** p : {&q[i], &k[i], &v[i], &o[i]}) CHECK(hipMalloc(p, n * 2));
+    CHECK(hipMalloc(&lse[i], static_cast<size_t>(s.B) * s.H * s.N * 4));
+    hipLaunchKernelGGL(fill, dim3(1024), dim3(256), 0, 0, static_cast<_Float16*>(q[i]), n, 3u * i + 1);
+    hipLaunchKernelGGL(fill, dim3(1024), dim3(256), 0, 0, static_cast<_Float16*>(k[i]), n, 3u * i + 2);
+    hipLaunchKernelGGL(fill, dim3(1024), dim3(256), 0, 0, static_cast<_Float16*>(v[i]), n, 3u * i + 3);
+  }
+  auto args = [&](int i) {
+    fa::KArgs a{};
+    a.q = q[i];
+    a.k = k[i];
+    a.v = v[i];
+    a.o = o[i];
+    a.lse = lse[i];
+    a.B = s.B;
+    a.H = s.H;
+    a.Hkv = s.H;
+    a.N = s.N;
+    a.scale = 1.0f / std::sqrt(static_cast<float>(s.D));
+    a.c = a.scale * 1.44269504088896341f;
+    a.causal = s.causal;
+    a.qsb = a.ksb = a.vsb = a.osb = static_cast<long long>(s.H) * s.N * s.D;
+    a.qsh = a.ksh = a.vsh = a.osh = static_cast<long long>(s.N) * s.D;
+    a.qsn = a.ksn = a.vsn = a.osn = s.D;
+    a.n_splits = 1;
+    a.fd_h = fa::make_fastdiv(s.H);
+    a.fd_group = fa::make_fastdiv(1);
+    a.fd_splits = fa::make_fastdiv(1);
+    return a;
+  };
+  hipStream_t st;
+  CHECK(hipStreamCreate(&st));
+  for (int i = 0; i < 20; ++i) CHECK(static_cast<hipError_t>(s.fn(args(i % kSets), st)));
+  hipEvent_t e0, e1;
+  CHECK(hipEventCreate(&e0));
+  CHECK(hipEventCreate(&e1));
+  CHECK(hipEventRecord(e0, st));
+  for (int i = 0; i < launches; ++i) CHECK(static_cast<hipError_t>(s.fn(args(i % kSets), st)));
+  CHECK(hipEventRecord(e1, st));
+  CHECK(hipEventSynchronize(e1));
+  float ms = 0.f;
+  CHECK(hipEventElapsedTime(&ms, e0, e1));
+  const double us = 1000.0 * ms / launches;
+
+  const int nwg = (s.N / 128) * s.B * s.H;
+  std::vector<unsigned long long> h(static_cast<size_t>(nwg) * 16 * 8);
+  CHECK(hipMemcpyFromSymbol(h.data(), HIP_SYMBOL(fa::m16::fa_phase_clocks), h.size() * 8));
+  double pro = 0, loop = 0, tail = 0, bar = 0, steps = 0, cyc = 0, rt = 0;
+  int nw = 0;
+  unsigned long long r_first = ~0ull, r_last_start = 0, r_first_end = ~0ull, r_last_end = 0;
+  for (int b = 0; b < nwg; ++b) {
+    for (int w = 0; w < 8; ++w) {
+      const unsigned long long* c = &h[(static_cast<size_t>(b) * 16 + w) * 8];
+      if (c[0] == 0 || c[3] < c[0]) continue;
+      ++nw;
+      pro += c[1] - c[0];
+      loop += c[2] - c[1];
+      tail += c[3] - c[2];
+      bar += c[4];
+      steps += c[7];
+      cyc += c[3] - c[0];
+      rt += c[6] - c[5];
+      r_first = std::min(r_first, c[5]);
+      r_last_start = std::max(r_last_start, c[5]);
+      r_first_end = std::min(r_first_end, c[6]);
+      r_last_end = std::max(r_last_end, c[6]);
+    }
+  }
+  if (nw == 0) {
+    std::printf("%s: no stamps recorded\n", s.name);
+    return;
+  }
+  const double flops = 4.0 * s.B * s.H * static_cast<double>(s.N) * s.N * s.D / (s.causal ? 2 : 1);
+  std::printf("%s (B%d H%d N%d D%d fp16%s, BR 128 x BC %d, %d workgroups x 8 waves):\n", s.name,
+              s.B, s.H, s.N, s.D, s.causal ? " causal" : "", s.bc, nwg);
+  std::printf("  launch (back to back, %d launches): %.2f us, %.1f TFLOP/s = %.1f %% of 2.5 PFLOP/s\n",
+              launches, us, flops / us * 1e-6, flops / us * 1e-6 / 25.0);
+  std::printf("  shader clock %.2f GHz; workgroup lifetime %.2f us; span first start -> last end "
+              "%.2f us; last start +%.2f us; first end +%.2f us\n",
+              cyc / (rt * 10.0), rt / nw * 0.01, (r_last_end - r_first) * 0.01,
+              (r_last_start - r_first) * 0.01, (r_first_end - r_first) * 0.01);
+  std::printf("  per wave (cycles): prologue %.0f | key walk %.0f = %.1f steps x %.0f "
+              "(barrier wait %.0f per step) | merge + epilogue %.0f | total %.0f\n",
+              pro / nw, loop / nw, steps / nw, loop / steps, bar / steps, tail / nw, cyc / nw);
+  for (int i = 0; i < kSets; ++i) {
+    for (void* p : {q[i], k[i], v[i], o[i]}) CHECK(hipFree(p));
+    CHECK(hipFree(lse[i]));
+  }
+  CHECK(hipStreamDestroy(st));
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const std::string which = argc > 1 ? argv[1] : "all";
+  const int launches = argc > 2 ? std::max(1, std::atoi(argv[2])) : 200;
+  bool any = false;
+  for (const Shape& s : kShapes) {
+    if (which == "all" || which == s.name) {
+      run(s, launches);
+      any = true;
+    }
+  }
+  if (!any) {
+    std::fprintf(stderr, "usage: phase_clocks [C64|C128|C128_causal|all] [launches]\n");
+    return 2;
+  }
+  return 0;
+}

@@ -77,6 +77,21 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef s16x4 __attribute__((address_space(3))) lds_s16x4;
 
 constexpr int kNumXcd = 8;
+
+// Phase clocks: a diagnostic build (bench/phase_clocks.hip defines FA_PHASE_CLOCKS) records, per
+// wave of stage 5, 8 words: s_memtime at the start, after the prologue barrier, after the key walk
+// and at the end; the s_memtime cycles spent in the step barriers (the wait for the slowest wave);
+// s_memrealtime (100 MHz) at the start and the end; the number of steps. The library itself is
+// built without it, and then none of this code exists.
+#if defined(FA_PHASE_CLOCKS)
+constexpr int kClockMaxWorkgroups = 4096;
+__device__ unsigned long long fa_phase_clocks[kClockMaxWorkgroups * 16 * 8];
+#define FA_CLK(i, v) clk[i] = (v)
+#define FA_CLK_ADD(i, v) clk[i] += (v)
+#else
+#define FA_CLK(i, v) ((void)0)
+#define FA_CLK_ADD(i, v) ((void)0)
+#endif
 constexpr float kLn2 = 0.69314718055994531f;
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -542,6 +557,21 @@ struct Fa16 {
     const int rg = wave % RG;
     const int ks = wave / RG;
     const int g = lane >> 5;
+#if defined(FA_PHASE_CLOCKS)
+    unsigned long long clk[8] = {};
+    const auto clk_store = [&] {
+      clk[3] = __builtin_amdgcn_s_memtime();
+      clk[6] = __builtin_amdgcn_s_memrealtime();
+      if (lane == 0 && PIPE && blockIdx.x < kClockMaxWorkgroups) {
+        unsigned long long* d = fa_phase_clocks + (static_cast<size_t>(blockIdx.x) * 16 + wave) * 8;
+        for (int i = 0; i < 8; ++i) d[i] = clk[i];
+      }
+    };
+    clk[0] = __builtin_amdgcn_s_memtime();
+    clk[5] = __builtin_amdgcn_s_memrealtime();
+#else
+    const auto clk_store = [] {};
+#endif
 
     // XCD-aware remap of the 1-D grid, then (head, q-tile) decode.
     const int G = gridDim.x;
@@ -658,6 +688,7 @@ struct Fa16 {
       }
       wait_dma();
       __syncthreads();  // V(t0), K(t0+1) visible; K buffer 0 is refilled in iteration 0
+      FA_CLK(1, __builtin_amdgcn_s_memtime());
       // One pipeline step. `full` (a compile-time tag) selects the steady-state body: tiles t and
       // t+1 are full for every wave of the workgroup and carry no causal diagonal, so the body has
       // no per-block branches and the VALU softmax of S(t) interleaves with the MFMAs of S(t+1).
@@ -698,8 +729,13 @@ struct Fa16 {
             pv<false>(ws, P, vc, vl, nv, dg);
           }
         }
+#if defined(FA_PHASE_CLOCKS)
+        const unsigned long long clk_b = __builtin_amdgcn_s_memtime();
+#endif
         wait_dma();
         __syncthreads();
+        FA_CLK_ADD(4, __builtin_amdgcn_s_memtime() - clk_b);
+        FA_CLK_ADD(7, 1);
       };
       using Full = std::true_type;
       using Part = std::false_type;
@@ -752,6 +788,7 @@ struct Fa16 {
       }
     }
 
+    FA_CLK(2, __builtin_amdgcn_s_memtime());
     // ---- merge the KS partial states of each row group (LDS is free after the last barrier) ----
     if constexpr (KS > 1) {
       float* mg = reinterpret_cast<float*>(lds_raw);
@@ -766,7 +803,10 @@ struct Fa16 {
         dst[(kDB * 16 + 1) * 64 + lane] = ws.l;
       }
       __syncthreads();
-      if (ks > 0) return;
+      if (ks > 0) {
+        clk_store();
+        return;
+      }
 #pragma unroll
       for (int sp = 1; sp < KS; ++sp) {
         const float* src = mg + ((sp - 1) * RG + rg) * kMergeFloats;
@@ -790,7 +830,10 @@ struct Fa16 {
 
     // ---- epilogue: O = acc / l, lse = m*scale + ln l (ref:include/fa/softmax_math.cuh:58-71) ----
     const float lt = ws.l + __shfl_xor(ws.l, 32);
-    if (!wave_valid) return;
+    if (!wave_valid) {
+      clk_store();
+      return;
+    }
     const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
     if (S > 1) {
       // One part of a split walk: its normalised O in fp32 and its LSE (-inf when the part saw
@@ -813,6 +856,7 @@ struct Fa16 {
                                ? ws.m * a.scale + log2_hw(lt) * kLn2
                                : -__builtin_inff();
       }
+      clk_store();
       return;
     }
     T* orow = static_cast<T*>(a.o) + b * a.osb + h * a.osh + row * a.osn;
@@ -837,6 +881,7 @@ struct Fa16 {
           (lt > 0.f && ws.m != -__builtin_inff()) ? ws.m * a.scale + log2_hw(lt) * kLn2
                                                    : __builtin_inff();
     }
+    clk_store();
   }
 };
 
