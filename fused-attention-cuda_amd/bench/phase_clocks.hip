@@ -8,7 +8,7 @@
 // cycles of each phase, the cycles per key-tile step and the barrier wait per step, and the shader
 // clock (s_memtime cycles over s_memrealtime's 100 MHz).
 //
-//   usage: phase_clocks [C64|C128|C128_causal|all] [launches]
+//   usage: phase_clocks [C64|C128|C128_causal|LONG|GPT_attn|all] [launches]
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -39,17 +39,24 @@ namespace {
 struct Shape {
   const char* name;
   int B, H, N, D, causal;
-  fa::LaunchFn fn;  // the tile the library picks for this shape (BR 128; BC 128 / 64)
-  int bc;
+  bool bf16;
+  fa::LaunchFn fn;  // the tile the library picks for this shape
+  int br, bc, waves;
+  float std;        // input scale (LONG: 0.5, as the benchmark)
 };
 
 const Shape kShapes[] = {
-    {"C64", 2, 8, 2048, 64, 0, &fa::m16::launch<5, _Float16, 64, 4, 2, 64>, 128},
-    {"C128", 2, 8, 2048, 128, 0, &fa::m16::launch<5, _Float16, 128, 4, 2, 32>, 64},
-    {"C128_causal", 2, 8, 2048, 128, 1, &fa::m16::launch<5, _Float16, 128, 4, 2, 32>, 64},
+    {"C64", 2, 8, 2048, 64, 0, false, &fa::m16::launch<5, _Float16, 64, 4, 2, 64>, 128, 128, 8, 1.f},
+    {"C128", 2, 8, 2048, 128, 0, false, &fa::m16::launch<5, _Float16, 128, 4, 2, 32>, 128, 64, 8, 1.f},
+    {"C128_causal", 2, 8, 2048, 128, 1, false, &fa::m16::launch<5, _Float16, 128, 4, 2, 32>, 128, 64, 8, 1.f},
+    // LONG: BR 128 x BC 32, four waves, two workgroups per CU (the narrow D = 128 tile).
+    {"LONG", 1, 16, 8192, 128, 1, true, &fa::m16::launch<5, __bf16, 128, 4, 1, 32>, 128, 32, 4, 0.5f},
+    // GPT-2 attention shape: BR 64 x BC 64, four waves (the short-walk D = 64 tile).
+    {"GPT_attn", 8, 12, 1024, 64, 1, false, &fa::m16::launch<5, _Float16, 64, 2, 2, 32>, 64, 64, 4, 1.f},
 };
 
-__global__ void fill(_Float16* p, size_t n, uint32_t seed) {
+template <typename T>
+__global__ void fill(T* p, size_t n, uint32_t seed, float scale) {
   for (size_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += gridDim.x * 256ull) {
     uint32_t h = static_cast<uint32_t>(i) * 0x9E3779B1u ^ seed;
     h ^= h >> 16;
@@ -59,7 +66,7 @@ __global__ void fill(_Float16* p, size_t n, uint32_t seed) {
     h ^= h >> 16;
     // sum of two uniforms, centred: a bell-shaped value in (-1, 1)
     const float u = ((h & 0xFFFF) + (h >> 16)) * (1.0f / 65536.0f) - 1.0f;
-    p[i] = static_cast<_Float16>(1.7f * u);
+    p[i] = static_cast<T>(1.7f * scale * u);
   }
 }
 
@@ -71,9 +78,16 @@ void run(const Shape& s, int launches) {
   for (int i = 0; i < kSets; ++i) {
     for (void** p : {&q[i], &k[i], &v[i], &o[i]}) CHECK(hipMalloc(p, n * 2));
     CHECK(hipMalloc(&lse[i], static_cast<size_t>(s.B) * s.H * s.N * 4));
-    hipLaunchKernelGGL(fill, dim3(1024), dim3(256), 0, 0, static_cast<_Float16*>(q[i]), n, 3u * i + 1);
-    hipLaunchKernelGGL(fill, dim3(1024), dim3(256), 0, 0, static_cast<_Float16*>(k[i]), n, 3u * i + 2);
-    hipLaunchKernelGGL(fill, dim3(1024), dim3(256), 0, 0, static_cast<_Float16*>(v[i]), n, 3u * i + 3);
+    for (int t = 0; t < 3; ++t) {
+      void* dst = t == 0 ? q[i] : t == 1 ? k[i] : v[i];
+      if (s.bf16) {
+        hipLaunchKernelGGL(fill<__bf16>, dim3(1024), dim3(256), 0, 0, static_cast<__bf16*>(dst), n,
+                           3u * i + t + 1, s.std);
+      } else {
+        hipLaunchKernelGGL(fill<_Float16>, dim3(1024), dim3(256), 0, 0, static_cast<_Float16*>(dst),
+                           n, 3u * i + t + 1, s.std);
+      }
+    }
   }
   auto args = [&](int i) {
     fa::KArgs a{};
@@ -112,14 +126,14 @@ void run(const Shape& s, int launches) {
   CHECK(hipEventElapsedTime(&ms, e0, e1));
   const double us = 1000.0 * ms / launches;
 
-  const int nwg = (s.N / 128) * s.B * s.H;
+  const int nwg = (s.N / s.br) * s.B * s.H;
   std::vector<unsigned long long> h(static_cast<size_t>(nwg) * 16 * 8);
   CHECK(hipMemcpyFromSymbol(h.data(), HIP_SYMBOL(fa::m16::fa_phase_clocks), h.size() * 8));
   double pro = 0, loop = 0, tail = 0, bar = 0, steps = 0, cyc = 0, rt = 0;
   int nw = 0;
   unsigned long long r_first = ~0ull, r_last_start = 0, r_first_end = ~0ull, r_last_end = 0;
   for (int b = 0; b < nwg; ++b) {
-    for (int w = 0; w < 8; ++w) {
+    for (int w = 0; w < s.waves; ++w) {
       const unsigned long long* c = &h[(static_cast<size_t>(b) * 16 + w) * 8];
       if (c[0] == 0 || c[3] < c[0]) continue;
       ++nw;
@@ -141,8 +155,9 @@ void run(const Shape& s, int launches) {
     return;
   }
   const double flops = 4.0 * s.B * s.H * static_cast<double>(s.N) * s.N * s.D / (s.causal ? 2 : 1);
-  std::printf("%s (B%d H%d N%d D%d fp16%s, BR 128 x BC %d, %d workgroups x 8 waves):\n", s.name,
-              s.B, s.H, s.N, s.D, s.causal ? " causal" : "", s.bc, nwg);
+  std::printf("%s (B%d H%d N%d D%d %s%s, BR %d x BC %d, %d workgroups x %d waves):\n", s.name,
+              s.B, s.H, s.N, s.D, s.bf16 ? "bf16" : "fp16", s.causal ? " causal" : "", s.br, s.bc,
+              nwg, s.waves);
   std::printf("  launch (back to back, %d launches): %.2f us, %.1f TFLOP/s = %.1f %% of 2.5 PFLOP/s\n",
               launches, us, flops / us * 1e-6, flops / us * 1e-6 / 25.0);
   std::printf("  shader clock %.2f GHz; workgroup lifetime %.2f us; span first start -> last end "
@@ -172,7 +187,7 @@ int main(int argc, char** argv) {
     }
   }
   if (!any) {
-    std::fprintf(stderr, "usage: phase_clocks [C64|C128|C128_causal|all] [launches]\n");
+    std::fprintf(stderr, "usage: phase_clocks [C64|C128|C128_causal|LONG|GPT_attn|all] [launches]\n");
     return 2;
   }
   return 0;
