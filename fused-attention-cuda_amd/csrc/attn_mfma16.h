@@ -46,8 +46,9 @@
 //
 // Grid: 1-D, (ceil(N/BR) * B * H) workgroups. Hardware hands workgroup i to XCD i % 8 (each XCD
 // has its own L2); blockIdx is remapped so that each XCD receives a contiguous range of
-// (head, q-tile) pairs and a head's K/V is fetched into one L2. Causal problems issue the longest
-// key ranges first. Causal key tiles past the workgroup's last row are never loaded; per wave,
+// (head, q-tile) pairs and a head's K/V is fetched into one L2 (layout::grid_item). Causal
+// problems issue the longest key ranges first, across all heads of an XCD's range when that range
+// is whole heads. Causal key tiles past the workgroup's last row are never loaded; per wave,
 // 32-key blocks past the wave's last row are skipped and only the diagonal block is masked.
 #pragma once
 
@@ -75,8 +76,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef s16x4 __attribute__((address_space(3))) lds_s16x4;
-
-constexpr int kNumXcd = 8;
 
 // Phase clocks: a diagnostic build (bench/phase_clocks.hip defines FA_PHASE_CLOCKS) records, per
 // wave of stage 5, 8 words: s_memtime at the start, after the prologue barrier, after the key walk
@@ -580,23 +579,19 @@ struct Fa16 {
     const auto clk_store = [] {};
 #endif
 
-    // XCD-aware remap of the 1-D grid, then (head, q-tile) decode.
-    const int G = gridDim.x;
-    const int bid = blockIdx.x;
-    const int xcd = bid % kNumXcd;
-    const int per = G / kNumXcd;
-    const int rem = G % kNumXcd;
-    const int logical =
-        (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + bid / kNumXcd;
-    // With split key walks the n_splits parts of one query tile are consecutive items.
-    // (readfirstlane: uniform integer divisions run on the vector unit, and their results would
-    // otherwise occupy vector registers for the whole kernel.)
+    // XCD-aware decode of the 1-D grid into (head, query tile, part). (readfirstlane: uniform
+    // integer divisions run on the vector unit, and their results would otherwise occupy vector
+    // registers for the whole kernel.)
+    const layout::Item item = layout::grid_item(
+        static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), a.n_qtiles, a.n_splits,
+        a.causal != 0, a.xcd_heads,
+        [&](int x) { return __builtin_amdgcn_readfirstlane(fdiv(x, a.fd_splits)); },
+        [&](int x) { return __builtin_amdgcn_readfirstlane(fdiv(x, a.fd_qtiles)); },
+        [&](int x) { return __builtin_amdgcn_readfirstlane(fdiv(x, a.fd_xcd_heads)); });
     const int S = a.n_splits;
-    const int item = __builtin_amdgcn_readfirstlane(fdiv(logical, a.fd_splits));
-    const int part = logical - item * S;
-    const int bh = fdiv(item, a.fd_qtiles);
-    int qt = item - bh * a.n_qtiles;
-    if (a.causal) qt = a.n_qtiles - 1 - qt;  // longest key ranges first
+    const int part = __builtin_amdgcn_readfirstlane(item.part);
+    const int bh = __builtin_amdgcn_readfirstlane(item.bh);
+    const int qt = __builtin_amdgcn_readfirstlane(item.qt);
     const int b = fdiv(bh, a.fd_h);
     const int h = bh - b * a.H;
     const int hk = fdiv(h, a.fd_group);
@@ -986,6 +981,8 @@ int launch(const KArgs& in, hipStream_t stream) {
   KArgs a = in;
   a.n_qtiles = (a.N + A::kBr - 1) / A::kBr;
   a.fd_qtiles = make_fastdiv(static_cast<uint32_t>(a.n_qtiles));
+  a.xcd_heads = layout::xcd_heads_for(a.B * a.H, a.causal != 0);
+  a.fd_xcd_heads = make_fastdiv(static_cast<uint32_t>(a.xcd_heads > 0 ? a.xcd_heads : 1));
   if (a.n_splits < 1 || (a.n_splits > 1 && (STAGE != 5 || a.o_part == nullptr ||
                                             a.lse_part == nullptr))) {
     return static_cast<int>(hipErrorInvalidValue);

@@ -75,6 +75,10 @@ struct KArgs {
   float* lse_part;
   // Divisors of the grid decode (see FastDiv): n_qtiles, H, H / Hkv and n_splits.
   FastDiv fd_qtiles, fd_h, fd_group, fd_splits;
+  // Stage 4/5 grid order (layout::grid_item): heads per XCD for the tile-major order, 0 for
+  // head-major; filled in by the launcher with its divisor.
+  int xcd_heads;
+  FastDiv fd_xcd_heads;
 };
 
 // Most parts a split key walk is cut into (fa_s5_combine holds one register set per part).

@@ -99,5 +99,55 @@ FA_HD inline Walk plan_walk(int N, int BC, int BR, int qt, bool causal, int part
   return w;
 }
 
+// The work item of workgroup `bid` of a stage-4/5 grid of G = n_qtiles * BH * splits workgroups
+// (BH = B * H): its batch-head bh, query tile qt and part of a split walk. The hardware hands
+// workgroup i to XCD i % kXcds, and each XCD has its own L2, so each XCD receives a contiguous
+// range of items and fetches a head's K/V into one L2. Inside an XCD's range:
+//  - head-major (xcd_heads == 0): items (bh, qt, part) in order;
+//  - tile-major (xcd_heads = BH / kXcds, only when kXcds divides BH): the range is xcd_heads
+//    whole heads, issued one query tile of all of them at a time. On a causal grid that issues
+//    the range's longest walks first (list scheduling, longest first); head-major issues them
+//    head by head, so the long tiles of an XCD's last heads start after the short tiles of its
+//    first ones.
+// Causal grids count qt down, longest key walk first. The parts of one query tile are
+// consecutive items in both orders. div_*(x) must return x / splits, x / n_qtiles and
+// x / xcd_heads (the kernel passes its multiply-shift divisions).
+constexpr int kXcds = 8;
+struct Item {
+  int bh;
+  int qt;
+  int part;
+};
+template <typename DivS, typename DivQ, typename DivX>
+FA_HD inline Item grid_item(int bid, int G, int n_qtiles, int splits, bool causal, int xcd_heads,
+                            DivS div_splits, DivQ div_qtiles, DivX div_xcd_heads) {
+  const int xcd = bid % kXcds;
+  const int local = bid / kXcds;
+  Item it;
+  int q;
+  if (xcd_heads > 0) {
+    const int item = div_splits(local);
+    it.part = local - item * splits;
+    q = div_xcd_heads(item);
+    it.bh = xcd * xcd_heads + (item - q * xcd_heads);
+  } else {
+    const int per = G / kXcds, rem = G % kXcds;
+    const int logical = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + local;
+    const int item = div_splits(logical);
+    it.part = logical - item * splits;
+    it.bh = div_qtiles(item);
+    q = item - it.bh * n_qtiles;
+  }
+  it.qt = causal ? n_qtiles - 1 - q : q;
+  return it;
+}
+
+// The launcher's choice of order: tile-major on causal grids whose BH splits into whole heads per
+// XCD, two or more of them (with one the orders coincide); head-major otherwise, where every
+// walk has the same length and the order only decides which heads share an L2.
+FA_HD constexpr int xcd_heads_for(int BH, bool causal) {
+  return (causal && BH % kXcds == 0 && BH / kXcds > 1) ? BH / kXcds : 0;
+}
+
 }  // namespace layout
 }  // namespace fa

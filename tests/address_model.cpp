@@ -15,7 +15,8 @@
 //     reads from that region stay inside it;
 //   * a split part's partial rows lie inside the workspace the library sizes for it.
 // Decode's split kernel (attn_decode.h) is replayed the same way: each split's keys [k_begin,
-// k_end) in 128-key tiles with the last tile clamped to the split's last key.
+// k_end) in 128-key tiles with the last tile clamped to the split's last key. The grid decode
+// (layout::grid_item) is checked to hand every workgroup a distinct in-range work item.
 // Exits non-zero on the first violation, printing the case.
 #include <cstdio>
 #include <cstdlib>
@@ -260,6 +261,65 @@ void sweep_decode() {
   }
 }
 
+// The grid decode (layout::grid_item) over a sweep of grids, in both orders: every workgroup gets
+// an in-range (bh, qt, part) and no two the same one (so all of them are covered); in the
+// tile-major order the parts of a query tile are issued one after another on one XCD, and each
+// XCD issues its causal query tiles longest first. The head-major order is checked to break that
+// last property on the same grids, which is why causal grids take the tile-major order, and which
+// shows the check can fail.
+void check_grid_items() {
+  for (int BH : {1, 3, 8, 16, 24, 96, 100}) {
+    for (int nq : {1, 2, 7, 16}) {
+      for (int S : {1, 2, 3}) {
+        for (bool causal : {false, true}) {
+          for (int order = 0; order < 2; ++order) {
+            const int xh = order ? fa::layout::xcd_heads_for(BH, causal) : 0;
+            if (order == 1 && xh == 0) continue;
+            const int G = nq * BH * S;
+            const std::string c = "grid BH=" + std::to_string(BH) + " nq=" + std::to_string(nq) +
+                                  " S=" + std::to_string(S) + (causal ? " causal" : "") +
+                                  (order ? " tile-major" : " head-major");
+            auto decode = [&](int bid) {
+              return fa::layout::grid_item(
+                  bid, G, nq, S, causal, xh, [S](int v) { return v / S; },
+                  [nq](int v) { return v / nq; }, [xh](int v) { return xh > 0 ? v / xh : 0; });
+            };
+            std::vector<char> seen(static_cast<size_t>(G), 0);
+            std::vector<std::vector<int>> issued(fa::layout::kXcds);  // qt per XCD, issue order
+            for (int bid = 0; bid < G; ++bid) {
+              const auto it = decode(bid);
+              if (it.bh < 0 || it.bh >= BH || it.qt < 0 || it.qt >= nq || it.part < 0 ||
+                  it.part >= S) {
+                fail("grid item out of range: " + c);
+              }
+              char& s = seen[static_cast<size_t>((it.bh * nq + it.qt) * S + it.part)];
+              if (s) fail("grid item issued twice: " + c);
+              s = 1;
+              if (order == 1 && it.part + 1 < S) {
+                const auto nx = decode(bid + fa::layout::kXcds);
+                if (nx.bh != it.bh || nx.qt != it.qt || nx.part != it.part + 1) {
+                  fail("parts of a query tile not consecutive on one XCD: " + c);
+                }
+              }
+              if (it.part == 0) issued[bid % fa::layout::kXcds].push_back(it.qt);
+              ++g_checks;
+            }
+            if (!causal) continue;
+            bool longest_first = true;
+            for (const auto& q : issued) {
+              for (size_t i = 1; i < q.size(); ++i) longest_first &= q[i] <= q[i - 1];
+            }
+            if (order == 1 && !longest_first) fail("tile-major order not longest first: " + c);
+            if (order == 0 && fa::layout::xcd_heads_for(BH, true) > 1 && nq > 1 && longest_first) {
+              fail("head-major order unexpectedly longest first: " + c);
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -279,6 +339,8 @@ int main(int argc, char** argv) {
   }
   sweep_decode<64>();
   sweep_decode<128>();
-  std::printf("address model: %d variants and decode, %lld checks, all in bounds\n", n, g_checks);
+  check_grid_items();
+  std::printf("address model: %d variants, decode and the grid decode, %lld checks, all in bounds\n",
+              n, g_checks);
   return 0;
 }
