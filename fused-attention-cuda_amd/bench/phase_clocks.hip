@@ -48,7 +48,8 @@ struct Shape {
 const Shape kShapes[] = {
     {"C64", 2, 8, 2048, 64, 0, false, &fa::m16::launch<5, _Float16, 64, 4, 2, 64>, 128, 128, 8, 1.f},
     {"C128", 2, 8, 2048, 128, 0, false, &fa::m16::launch<5, _Float16, 128, 4, 2, 32>, 128, 64, 8, 1.f},
-    {"C128_causal", 2, 8, 2048, 128, 1, false, &fa::m16::launch<5, _Float16, 128, 4, 2, 32>, 128, 64, 8, 1.f},
+    // Causal C128: the library halves the height (BR 64 x BC 64, 512 workgroups issued tile-major).
+    {"C128_causal", 2, 8, 2048, 128, 1, false, &fa::m16::launch<5, _Float16, 128, 2, 2, 32>, 64, 64, 4, 1.f},
     // LONG: BR 128 x BC 32, four waves, two workgroups per CU (the narrow D = 128 tile).
     {"LONG", 1, 16, 8192, 128, 1, true, &fa::m16::launch<5, __bf16, 128, 4, 1, 32>, 128, 32, 4, 0.5f},
     // GPT-2 attention shape: BR 64 x BC 64, four waves (the short-walk D = 64 tile).

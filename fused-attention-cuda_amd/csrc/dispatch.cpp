@@ -20,6 +20,7 @@
 
 #include "fa/attention.h"
 #include "fa_internal.h"
+#include "tile_layout.h"
 
 namespace fa {
 namespace {
@@ -304,21 +305,29 @@ bool d64_narrow_s5(const fa_params& p, long long cus) {
   return grid64 >= 3 * cus;
 }
 
+// Causal grids whose B * H is a multiple of the XCD count are issued tile-major: each XCD issues
+// the longest query tile of all its heads, then the next-longest (layout::grid_item), so
+// workgroups of unequal length pair up on a CU. Other grids are issued head by head.
+bool tile_major_s5(const fa_params& p) {
+  return layout::xcd_heads_for(p.B * p.H, p.causal != 0) > 0;
+}
+
 // D = 128 with one key split of 32 keys per 32-row wave (BC 32; BR 128 is a 4-wave workgroup
 // with no key-split merge). Taken when the grid holds at least two BR-128 workgroups per CU:
 // two 4-wave workgroups then share each CU without a common barrier. Measured
 // (profiles/tile_rule_d128_narrow_s5.md, us, against BC 64): B8 H32 N1024 fp16 200.0 against
 // 242.3; LONG (B1 H16 N8192 bf16 causal) 355.5 against 405.8. C128 (B2 H8 N2048, one workgroup
 // per CU, which would leave one wave per SIMD) stays at BC 64 (43.0 against 51.0; causal 37.1
-// against 47.6). Causal long walks need four per CU: with two, the two workgroups resident on a
-// CU are tiles of equal length from two heads, so the CUs holding the longest tiles hold two of
-// them (B1 H16 N4096 bf16 causal: 115.1 at BC 64 against 135.9), where the 8-wave kernel hands
-// tiles to CUs as they free up.
+// against 47.6). Causal long walks need more: with two per CU, the CUs that hold the longest
+// tiles run two long walks side by side, where the 8-wave kernel hands tiles to CUs as they free
+// up (B1 H16 N4096 causal, issued tile-major: 74.9 us at BC 64 against 90.2). Issued tile-major,
+// three per CU are enough (B8 H12 N1024 fp16 causal: 41.4 against 47.7 at BC 64); issued head by
+// head, the threshold measured before the tile-major order existed is four.
 bool d128_narrow_s5(const fa_params& p, long long cus) {
   if (p.D != 128) return false;
   const long long grid128 = static_cast<long long>(p.B) * p.H * ((p.N + 127) / 128);
   if (grid128 < 2 * cus) return false;
-  return !p.causal || short_walk_s5(p) || grid128 >= 4 * cus;
+  return !p.causal || short_walk_s5(p) || grid128 >= (tile_major_s5(p) ? 3 : 4) * cus;
 }
 
 // Stage-5 key-tile width when FA_FORCE_BC is unset. It does not depend on the height, so a
@@ -329,9 +338,20 @@ int auto_bc_s5(const fa_params& p, long long cus) {
   return default_bc_mfma(p.D);
 }
 
+// Causal grids issued tile-major with fewer than two BR-128 workgroups per CU take BR 64 as well:
+// at one per CU the launch lasts as long as the longest query tile's walk, while 64-row
+// workgroups, two or more per CU in tile-major order, pair a long tile with a short one on each
+// CU. Measured (eager, fp16, us, BR 128 against BR 64 at the automatic width): C64 causal
+// (B2 H8 N2048 D64) 21.5 against 19.0, C128 causal (D128) 33.3 against 31.0. Where BR 128 already
+// puts two per CU it stays (B1 H16 N4096 D128 causal 74.9 against 81.6).
+bool causal_halve_s5(const fa_params& p, long long cus) {
+  const long long grid128 = static_cast<long long>(p.B) * p.H * ((p.N + 127) / 128);
+  return tile_major_s5(p) && grid128 < 2 * cus;
+}
+
 // `cus`: the compute units to fill (the current device's for a launch).
 int auto_br_s5(VariantList list, const fa_params& p, int bc, long long cus) {
-  const bool short_walk = short_walk_s5(p) || d64_narrow_s5(p, cus);
+  const bool short_walk = short_walk_s5(p) || d64_narrow_s5(p, cus) || causal_halve_s5(p, cus);
   for (const int br : {128, 64}) {
     if (find_variant(list, p.D, br, bc) == nullptr) continue;
     if (br == 128 && short_walk && find_variant(list, p.D, 64, bc) != nullptr) continue;

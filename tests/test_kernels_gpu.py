@@ -118,14 +118,20 @@ def test_stage5_default_height_matches_forced_heights(b, h, n, d, dtype, causal,
 
 # The tile stage 5 picks by itself on grids that fill a 256-CU device (csrc/dispatch.cpp,
 # auto_bc_s5 / auto_br_s5): narrow tiles where several workgroups share a CU, except for causal
-# long walks at D = 128 with fewer than four BR-128 workgroups per CU.
+# long walks at D = 128 with fewer than three BR-128 workgroups per CU (grids issued tile-major,
+# B * H a multiple of 8). The height never changes results, so the comparison with the forced tile
+# pins the width; the forced tile names the height the rules pick too.
 @pytest.mark.parametrize("b,h,n,d,dtype,causal,tile", [
     (8, 32, 1024, 64, torch.float16, False, (64, 64)),      # D = 64, 16 per CU
     (4, 32, 512, 128, torch.float16, False, (128, 32)),     # D = 128, 2 per CU
     (4, 32, 512, 128, torch.bfloat16, True, (64, 32)),      # short causal walks
     (2, 8, 4096, 128, torch.float16, True, (128, 64)),      # causal long walks, 2 per CU
+    (8, 12, 1024, 128, torch.float16, True, (128, 32)),     # causal, 3 per CU, tile-major
     (1, 16, 8192, 128, torch.bfloat16, True, (128, 32)),    # LONG: causal, 4 per CU
-], ids=["d64-large", "d128-dense", "d128-short-causal", "d128-causal-2cu", "long"])
+    (2, 8, 2048, 64, torch.float16, True, (64, 128)),       # C64 causal: halved height
+    (2, 8, 2048, 128, torch.float16, True, (64, 64)),       # C128 causal: halved height
+], ids=["d64-large", "d128-dense", "d128-short-causal", "d128-causal-2cu", "d128-causal-3cu",
+        "long", "c64-causal", "c128-causal"])
 def test_stage5_automatic_tile_on_full_grids(b, h, n, d, dtype, causal, tile, make_qkv,
                                              reset_overrides):
     require(5, dtype, d)
