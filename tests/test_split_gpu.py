@@ -7,7 +7,8 @@ The library splits where its cost model says the GPU would otherwise sit idle (o
 a head-sharded problem); ``FA_FORCE_SPLITS`` forces S for these tests.
 
 * Forced S in {2, 3, 5} on full and causal problems, fp16 and bf16, D 64 and 128, with N an odd
-  multiple of 32 (partial tiles), against the fp64 oracle at the stated tolerance.
+  multiple of 32 (partial tiles), against the fp64 oracle at the stated tolerance; one shape has
+  B * H a multiple of 8, whose causal grid is issued tile-major.
 * More parts than key tiles: the empty parts carry LSE = -inf and weigh nothing.
 * The shapes the model splits by itself: the C-ABI asks for a workspace, and the op
   (``torch.ops.fused_attn.forward``, which allocates what ``fa_workspace_bytes`` asks for) and the
@@ -53,7 +54,10 @@ def _split_run(q, k, v, causal, scale):
 
 @pytest.mark.parametrize("splits", [2, 3, 5])
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
-@pytest.mark.parametrize("b,h,n,d", [(1, 2, 352, 64), (2, 3, 224, 128), (1, 1, 1024, 64)],
+# (2, 8, 288, 64): B * H a multiple of 8, so the causal runs are issued tile-major
+# (layout::grid_item) with the parts of each query tile consecutive on one XCD.
+@pytest.mark.parametrize("b,h,n,d", [(1, 2, 352, 64), (2, 3, 224, 128), (1, 1, 1024, 64),
+                                     (2, 8, 288, 64)],
                          ids=lambda x: str(x))
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
 def test_forced_splits_match_oracle(b, h, n, d, dtype, causal, splits, monkeypatch):
