@@ -142,7 +142,7 @@ void run(const Shape& s, int launches) {
       loop += c[2] - c[1];
       tail += c[3] - c[2];
       bar += c[4];
-      steps += c[7];
+      steps += static_cast<double>(c[7] & 0xffffffffull);
       cyc += c[3] - c[0];
       rt += c[6] - c[5];
       r_first = std::min(r_first, c[5]);
@@ -168,6 +168,37 @@ void run(const Shape& s, int launches) {
   std::printf("  per wave (cycles): prologue %.0f | key walk %.0f = %.1f steps x %.0f "
               "(barrier wait %.0f per step) | merge + epilogue %.0f | total %.0f\n",
               pro / nw, loop / nw, steps / nw, loop / steps, bar / steps, tail / nw, cyc / nw);
+  // Per XCD (hardware XCC_ID of wave 0 of each workgroup): how many workgroups ran there, whether
+  // workgroup i ran on XCD i % 8 (the grid remap assumes it), and when they started and ended
+  // (us after the first start), with the mean lifetime and shader clock.
+  int mismatch = 0;
+  std::printf("  per XCD: wgs | start first/last | end first/mean/last | lifetime mean | clock\n");
+  for (int xcd = 0; xcd < 8; ++xcd) {
+    int n = 0;
+    double life = 0, endsum = 0, cycs = 0, rts = 0;
+    unsigned long long s0 = ~0ull, s1 = 0, e0 = ~0ull, e1 = 0;
+    for (int b = 0; b < nwg; ++b) {
+      const unsigned long long* c = &h[static_cast<size_t>(b) * 16 * 8];
+      if (c[0] == 0 || c[3] < c[0]) continue;
+      const int hx = static_cast<int>((c[7] >> 32) & 15u);
+      if (xcd == 0 && hx != b % 8) ++mismatch;
+      if (hx != xcd) continue;
+      ++n;
+      life += c[6] - c[5];
+      endsum += c[6] - r_first;
+      cycs += c[3] - c[0];
+      rts += c[6] - c[5];
+      s0 = std::min(s0, c[5]);
+      s1 = std::max(s1, c[5]);
+      e0 = std::min(e0, c[6]);
+      e1 = std::max(e1, c[6]);
+    }
+    if (n == 0) continue;
+    std::printf("    XCD %d: %4d | +%.2f / +%.2f | +%.2f / +%.2f / +%.2f | %.2f us | %.2f GHz\n", xcd,
+                n, (s0 - r_first) * 0.01, (s1 - r_first) * 0.01, (e0 - r_first) * 0.01,
+                endsum / n * 0.01, (e1 - r_first) * 0.01, life / n * 0.01, cycs / (rts * 10.0));
+  }
+  std::printf("  workgroups not on XCD (index %% 8): %d of %d\n", mismatch, nwg);
   for (int i = 0; i < kSets; ++i) {
     for (void* p : {q[i], k[i], v[i], o[i]}) CHECK(hipFree(p));
     CHECK(hipFree(lse[i]));

@@ -80,8 +80,10 @@ typedef s16x4 __attribute__((address_space(3))) lds_s16x4;
 // Phase clocks: a diagnostic build (bench/phase_clocks.hip defines FA_PHASE_CLOCKS) records, per
 // wave of stage 5, 8 words: s_memtime at the start, after the prologue barrier, after the key walk
 // and at the end; the s_memtime cycles spent in the step barriers (the wait for the slowest wave);
-// s_memrealtime (100 MHz) at the start and the end; the number of steps. The library itself is
-// built without it, and then none of this code exists.
+// s_memrealtime (100 MHz) at the start and the end; the number of steps in the low 32 bits of the
+// last word, with the wave's XCC (hardware register XCC_ID, 4 bits) at bit 32 and the low 24 bits
+// of its HW_ID (wave, SIMD, CU, shader array and engine) at bit 40. The library itself is built
+// without it, and then none of this code exists.
 #if defined(FA_PHASE_CLOCKS)
 constexpr int kClockMaxWorkgroups = 4096;
 __device__ unsigned long long fa_phase_clocks[kClockMaxWorkgroups * 16 * 8];
@@ -568,6 +570,10 @@ struct Fa16 {
     const auto clk_store = [&] {
       clk[3] = __builtin_amdgcn_s_memtime();
       clk[6] = __builtin_amdgcn_s_memrealtime();
+      // s_getreg operand: register id | offset << 6 | (bits - 1) << 11; XCC_ID is 20, HW_ID 4.
+      const unsigned long long xcc = __builtin_amdgcn_s_getreg(20 | (3 << 11)) & 15u;
+      const unsigned long long hw = __builtin_amdgcn_s_getreg(4 | (31 << 11)) & 0xffffffu;
+      clk[7] = (clk[7] & 0xffffffffull) | (xcc << 32) | (hw << 40);
       if (lane == 0 && PIPE && blockIdx.x < kClockMaxWorkgroups) {
         unsigned long long* d = fa_phase_clocks + (static_cast<size_t>(blockIdx.x) * 16 + wave) * 8;
         for (int i = 0; i < 8; ++i) d[i] = clk[i];
