@@ -694,6 +694,16 @@ struct Fa16 {
         const int nv0 = nvalid_of(t0);
         if (nv0 > 0) qk<false>(sa, ws, kwave(0), nv0, kl);
       }
+      // When the first step is a steady one (tile t0 full and free of the causal diagonal), the
+      // reference max starts at the row max of S(t0), taken here. Otherwise the first step
+      // exponentiates against m = -inf, finds no reference and redoes the tile: once per walk,
+      // in both precisions. The results are the same: the redo moved m to this max and scaled
+      // the still-empty l and O by 0.
+      if (__builtin_amdgcn_readfirstlane(walk.n_steady) > t0) {
+        const float mx = tile_max<true>(sa, kKB);
+        ws.m = mx;
+        ws.mc = (mx == -__builtin_inff()) ? 0.f : mx * c;
+      }
       wait_dma();
       __syncthreads();  // V(t0), K(t0+1) visible; K buffer 0 is refilled in iteration 0
       FA_CLK(1, __builtin_amdgcn_s_memtime());
