@@ -321,8 +321,9 @@ bool tile_major_s5(const fa_params& p) {
 // against 47.6). Causal long walks need more: with two per CU, the CUs that hold the longest
 // tiles run two long walks side by side, where the 8-wave kernel hands tiles to CUs as they free
 // up (B1 H16 N4096 causal, issued tile-major: 74.9 us at BC 64 against 90.2). Issued tile-major,
-// three per CU are enough (B8 H12 N1024 fp16 causal: 41.4 against 47.7 at BC 64); issued head by
-// head, the threshold measured before the tile-major order existed is four.
+// three per CU are enough (profiles/tile_rule_causal_s5.md; B8 H12 N1024 fp16 causal: 41.4
+// against 47.7 at BC 64); issued head by head, the threshold measured before the tile-major
+// order existed is four.
 bool d128_narrow_s5(const fa_params& p, long long cus) {
   if (p.D != 128) return false;
   const long long grid128 = static_cast<long long>(p.B) * p.H * ((p.N + 127) / 128);
@@ -341,9 +342,10 @@ int auto_bc_s5(const fa_params& p, long long cus) {
 // Causal grids issued tile-major with fewer than two BR-128 workgroups per CU take BR 64 as well:
 // at one per CU the launch lasts as long as the longest query tile's walk, while 64-row
 // workgroups, two or more per CU in tile-major order, pair a long tile with a short one on each
-// CU. Measured (eager, fp16, us, BR 128 against BR 64 at the automatic width): C64 causal
-// (B2 H8 N2048 D64) 21.5 against 19.0, C128 causal (D128) 33.3 against 31.0. Where BR 128 already
-// puts two per CU it stays (B1 H16 N4096 D128 causal 74.9 against 81.6).
+// CU. Measured (profiles/tile_rule_causal_s5.md; eager, fp16, us, BR 128 against BR 64 at the
+// automatic width): C64 causal (B2 H8 N2048 D64) 21.5 against 19.0, C128 causal (D128) 33.3
+// against 31.0. Where BR 128 already puts two per CU it stays (B1 H16 N4096 D128 causal 74.9
+// against 81.6).
 bool causal_halve_s5(const fa_params& p, long long cus) {
   const long long grid128 = static_cast<long long>(p.B) * p.H * ((p.N + 127) / 128);
   return tile_major_s5(p) && grid128 < 2 * cus;
@@ -390,7 +392,8 @@ int width_for_forced_height(VariantList list, int D, int br, int auto_bc) {
 //              + (S > 1 ? combine : 0)
 //   combine  = (2 S + 0.5) * rows * D * 4 bytes at 4 TB/s (the parts written, read back, and O)
 //              + 2 us for the second launch.
-// The S in 2..16 with the least time is taken when it saves at least 20 % over S = 1. The model
+// The S in 2..16 with the least time is taken when it saves at least 20 % over S = 1
+// (profiles/tile_rule_s5_splits.md: the model's choice against the rejected alternative). The model
 // assumes MI355X's 256 CUs whatever the current device: S sets the workspace size, so it must
 // depend on the problem only (a workspace sized on one device stays valid on another). On MI355X
 // this splits one GPU's share of a head-sharded problem (2 heads of B2 H8 N2048 D64, 2 of
