@@ -199,6 +199,21 @@ void run(const Shape& s, int launches) {
                 endsum / n * 0.01, (e1 - r_first) * 0.01, life / n * 0.01, cycs / (rts * 10.0));
   }
   std::printf("  workgroups not on XCD (index %% 8): %d of %d\n", mismatch, nwg);
+  // With PHASE_CLOCKS_DUMP=<dir>, one CSV row per workgroup (wave 0): index, XCC, HW_ID and the
+  // s_memrealtime start and end, for offline study of where the dispatcher placed each workgroup.
+  if (const char* dir = std::getenv("PHASE_CLOCKS_DUMP")) {
+    const std::string path = std::string(dir) + "/" + s.name + ".csv";
+    if (FILE* f = std::fopen(path.c_str(), "w")) {
+      std::fprintf(f, "bid,xcc,hw_id,start,end\n");
+      for (int b = 0; b < nwg; ++b) {
+        const unsigned long long* c = &h[static_cast<size_t>(b) * 16 * 8];
+        if (c[0] == 0) continue;
+        std::fprintf(f, "%d,%llu,%llu,%llu,%llu\n", b, (c[7] >> 32) & 15u, c[7] >> 40,
+                     c[5] - r_first, c[6] - r_first);
+      }
+      std::fclose(f);
+    }
+  }
   for (int i = 0; i < kSets; ++i) {
     for (void* p : {q[i], k[i], v[i], o[i]}) CHECK(hipFree(p));
     CHECK(hipFree(lse[i]));
