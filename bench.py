@@ -183,11 +183,14 @@ def time_steps(torch, capi, args_list, causal, scale, stage, stream, steps, warm
     return start.elapsed_time(end) / steps
 
 
-def graph_timing(torch, capi, args_list, causal, scale, stage, stream, steps):
+def graph_timing(torch, capi, args_list, causal, scale, stage, stream, steps, repeats=1):
     """The same ``steps`` launches captured once into a HIP graph (torch.cuda.CUDAGraph on the
     launch stream) and replayed: the execution mode of a serving loop. Before timing, the graph is
     replayed twice with the outputs cleared in between and every output compared bitwise with one
-    eager launch per input set (the kernel is deterministic). Returns ms per launch."""
+    eager launch per input set (the kernel is deterministic). Returns ms per launch of one timed
+    replay, or with ``repeats`` = 3 the median of three (the configuration rows: one transient, a
+    clock dip or a stall of the box, then cannot set a row on its own). The headline keeps one
+    bracketed replay of exactly K launches."""
     with torch.cuda.stream(stream):  # one eager launch per set: the reference outputs
         for q, k, v, o, lse in args_list:
             capi.forward(stage, q, k, v, o, lse, causal, scale, stream=stream,
@@ -211,15 +214,18 @@ def graph_timing(torch, capi, args_list, causal, scale, stage, stream, steps):
         for (o_ref, l_ref), (_, _, _, o, lse) in zip(eager, args_list):
             if not (torch.equal(o, o_ref) and torch.equal(lse, l_ref)):
                 raise RuntimeError("graph replay differs from the eager launches")
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        e0.record(stream)
-        graph.replay()
-        e1.record(stream)
-    e1.synchronize()
+    times = []
+    for _ in range(repeats):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            graph.replay()
+            e1.record(stream)
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1) / steps)
     del graph
-    return e0.elapsed_time(e1) / steps
+    return sorted(times)[len(times) // 2]
 
 
 # The MI355X last-level cache: 256 MB of Infinity Cache (MALL) in front of HBM, plus 8 x 4 MB L2.
@@ -351,7 +357,8 @@ def bench_workload(torch, capi, name, stage, steps, warmup, seed=0, gate_it=True
     err = gate(torch, capi, *sets[0], causal, scale, stage, stream) if gate_it else (None, None)
     eager_ms = time_steps(torch, capi, sets, causal, scale, stage, stream,
                           steps if eager else 0, warmup)
-    ms = graph_timing(torch, capi, sets, causal, scale, stage, stream, steps) if replay else None
+    ms = (graph_timing(torch, capi, sets, causal, scale, stage, stream, steps, repeats=3)
+          if replay else None)
     f = flops(b, h, n, d, causal)
     tf = f / (ms * 1e-3) / 1e12 if replay else None
     res = {"B": b, "H": h, "N": n, "D": d, "dtype": dt, "causal": causal, "stage": stage,
