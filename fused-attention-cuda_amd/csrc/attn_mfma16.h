@@ -534,7 +534,18 @@ struct Fa16 {
     constexpr int kMfma = kKB * (D / 16);
     constexpr int kVReads = kKB * 2 * kDB * 2;
     constexpr int kValu = (kF16 ? 48 : 66) * kKB;
-    constexpr int kPer = (kValu + kMfma - 1) / kMfma;
+    // VALU ops per MFMA: by default the step's softmax VALU spread evenly over the S(t+1) MFMAs
+    // (the rest issue after the last one). Tiles where fewer per MFMA measured faster
+    // (same-box A/B, eager launches, bit-identical outputs), against the even spread:
+    //   fp16 D64, two 32-key blocks per wave (C64's BR 128 x BC 128): 4 against 12,
+    //     C64 -3.4 to -3.9 %, C64 causal at BR 64 -2.7 %;
+    //   bf16 D128, one key split (LONG's BR 128 x BC 32): 4 against 9, -1.5 %.
+    // C128's tile keeps its 6 (3, 4 and 8 measured 1 to 2 % slower), and the GPT-2 attention
+    // shape's D64 tile with one block per wave its 12 (8: median of 12 pairs within 0.3 %).
+    constexpr int kPerEven = (kValu + kMfma - 1) / kMfma;
+    constexpr int kPer = (kF16 && D == 64 && kKB == 2)    ? 4
+                         : (!kF16 && D == 128 && KS == 1) ? 4
+                                                          : kPerEven;
     __builtin_amdgcn_sched_group_barrier(0x100, kMfma, 0);    // DS reads: K rows
     __builtin_amdgcn_sched_group_barrier(0x100, kVReads, 0);  // DS reads: V^T operands
     __builtin_amdgcn_sched_group_barrier(0x020, 2 * kDmaPerWave, 0);  // VMEM: the DMA
