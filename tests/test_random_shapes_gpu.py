@@ -1,0 +1,67 @@
+"""Seeded random shapes through stage 5 (marker ``gpu``).
+
+48 cases drawn once from a fixed seed cover:
+* batch 1-3 and 1-24 query heads, several of them multiples of 8, whose causal grids are issued
+  tile-major;
+* kv heads a divisor of the query heads (GQA/MQA);
+* N a multiple of 32 up to 640 (partial query and key tiles), D 64 or 128;
+* fp16 or bf16, causal or not;
+* for some, a forced split count of 2, 3 or 5, with the workspace the op sizes through
+  ``fa_workspace_bytes``.
+Each case runs on the tile the library picks by itself. Every head is checked against the fp64
+oracle at the stated tolerance (tests/_checks.py). The test id spells out the draw, so a failure
+names its shape.
+"""
+
+from __future__ import annotations
+
+import random
+
+import pytest
+import torch
+
+import fused_attn
+from _checks import check_against_reference
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"fp16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _draw(count: int = 48, seed: int = 20261202):
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(count):
+        b = rng.choice([1, 1, 2, 3])
+        h = rng.choice([1, 2, 3, 4, 6, 8, 12, 16, 24])
+        hkv = rng.choice([x for x in range(1, h + 1) if h % x == 0])
+        n = 32 * rng.randint(1, 20)
+        d = rng.choice([64, 128])
+        dt = rng.choice(sorted(DTYPES))
+        causal = rng.random() < 0.5
+        splits = rng.choice([0, 0, 0, 2, 3, 5])
+        cases.append((b, h, hkv, n, d, dt, causal, splits))
+    return cases
+
+
+def _case_id(c):
+    b, h, hkv, n, d, dt, causal, splits = c
+    return f"B{b}H{h}kv{hkv}N{n}D{d}{dt}{'-causal' if causal else ''}{f'-S{splits}' if splits else ''}"
+
+
+@pytest.mark.parametrize("case", _draw(), ids=_case_id)
+def test_random_shape_matches_oracle(case, make_qkv, monkeypatch):
+    if not fused_attn.is_available():
+        pytest.fail("fused_attn._C is not built: the HIP path must be the one that runs")
+    b, h, hkv, n, d, dt, causal, splits = case
+    dtype = DTYPES[dt]
+    if not fused_attn.impl_supports(5, dtype, d):
+        pytest.skip(f"stage 5 is not built for {dt} D={d} on this GPU")
+    if splits:
+        monkeypatch.setenv("FA_FORCE_SPLITS", str(splits))
+    else:
+        monkeypatch.delenv("FA_FORCE_SPLITS", raising=False)
+    q, k, v = make_qkv(b, h, n, d, dtype=dtype, device="cuda", hkv=hkv, seed=n + 7 * h + d)
+    o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
+    torch.cuda.synchronize()
+    check_against_reference(o, q, k, v, causal, dtype, lse=lse)
