@@ -293,16 +293,29 @@ bool short_walk_s5(const fa_params& p) {
 
 // D = 64 with 64-row workgroups and 32 keys per wave (BR 64, BC 64): 76 VGPRs and 32 KiB of LDS,
 // so up to five 4-wave workgroups share a CU where the default tile (104 VGPRs, 64 KiB) fits two.
-// Taken for short walks, and wherever the grid holds at least three such workgroups per CU.
-// Measured (profiles/tile_rule_d64_narrow_s5.md, fp16, us, against BR 128 / BC 128): the GPT-2
-// attention shape B8 H12 N1024 causal 32.9 against 43.4 (2.43 resident waves per busy SIMD
-// against 1.84); B8 H32 N2048 431.9 against 445.2. C64 (B2 H8 N2048, two narrow workgroups per
-// CU) stays at BR 128 / BC 128 (27.4 against 27.8).
-bool d64_narrow_s5(const fa_params& p, long long cus) {
+// fp16 takes it (profiles/tile_rule_d64_narrow_s5.md; eager launches, us, BR 64 / BC 64 against
+// BR 128 / BC 128, measured once the steady step's VALU groups were tuned for the wide tile):
+//  - for short walks;
+//  - for walks of at most about 8 wide key tiles on average (dense N <= 1024, causal N <= 2048)
+//    on grids of at least three narrow workgroups per CU: the GPT-2 attention shape (B8 H12 N1024
+//    causal) 24.9 against 29.3, B8 H16 N1024 causal 33.5 against 39.9, B1 H48 N2048 causal 41.0
+//    against 43.7, B8 H12 N1024 dense 38.6 against 40.5;
+//  - on grids of at least eight BR-128 workgroups per CU, whatever the walk: B8 H32 N2048 364.0
+//    against 373.6, B2 H32 N4096 337.8 against 345.1.
+// With fewer, on longer walks, the wide tile wins: B2 H8 N8192 302.6 against 329.9, B1 H32 N4096
+// 159.6 against 169.4, B4 H8 N2048 45.7 against 49.6, B1 H16 N8192 causal 161.4 against 170.4.
+// C64 (B2 H8 N2048) stays wide; causal C64 takes BR 64 at the wide width (causal_halve_s5).
+// bf16 keeps the rule measured before that tuning, three narrow workgroups per CU (B8 H8 N2048
+// dense, four BR-128 workgroups per CU: 99.0 against 101.3).
+bool d64_narrow_s5(const fa_params& p, int dtype, long long cus) {
   if (p.D != 64) return false;
   if (short_walk_s5(p)) return true;
-  const long long grid64 = static_cast<long long>(p.B) * p.H * ((p.N + 63) / 64);
-  return grid64 >= 3 * cus;
+  const long long bh = static_cast<long long>(p.B) * p.H;
+  const long long grid64 = bh * ((p.N + 63) / 64);
+  if (dtype != FA_DTYPE_F16) return grid64 >= 3 * cus;
+  const long long tiles = (p.N + 127) / 128;  // wide key tiles of the longest walk
+  const bool up_to_8 = (p.causal ? tiles + 1 : 2 * tiles) <= 17;  // twice the average walk
+  return (up_to_8 && grid64 >= 3 * cus) || bh * tiles >= 8 * cus;
 }
 
 // Causal grids whose B * H is a multiple of the XCD count are issued tile-major: each XCD issues
@@ -333,8 +346,8 @@ bool d128_narrow_s5(const fa_params& p, long long cus) {
 
 // Stage-5 key-tile width when FA_FORCE_BC is unset. It does not depend on the height, so a
 // forced height keeps the automatic width (and every height runs the same key split).
-int auto_bc_s5(const fa_params& p, long long cus) {
-  if (d64_narrow_s5(p, cus)) return 64;
+int auto_bc_s5(const fa_params& p, int dtype, long long cus) {
+  if (d64_narrow_s5(p, dtype, cus)) return 64;
   if (d128_narrow_s5(p, cus)) return 32;
   return default_bc_mfma(p.D);
 }
@@ -352,8 +365,9 @@ bool causal_halve_s5(const fa_params& p, long long cus) {
 }
 
 // `cus`: the compute units to fill (the current device's for a launch).
-int auto_br_s5(VariantList list, const fa_params& p, int bc, long long cus) {
-  const bool short_walk = short_walk_s5(p) || d64_narrow_s5(p, cus) || causal_halve_s5(p, cus);
+int auto_br_s5(VariantList list, const fa_params& p, int dtype, int bc, long long cus) {
+  const bool short_walk =
+      short_walk_s5(p) || d64_narrow_s5(p, dtype, cus) || causal_halve_s5(p, cus);
   for (const int br : {128, 64}) {
     if (find_variant(list, p.D, br, bc) == nullptr) continue;
     if (br == 128 && short_walk && find_variant(list, p.D, 64, bc) != nullptr) continue;
@@ -406,8 +420,8 @@ constexpr int kModelCus = 256;
 int s5_splits(const fa_params& p, int dtype) {
   if (const int f = env_positive_int("FA_FORCE_SPLITS")) return std::min(f, kMaxSplits);
   if (p.B < 1 || p.H < 1 || p.N < 1) return 1;
-  const int bc = auto_bc_s5(p, kModelCus);
-  const int br = auto_br_s5(s5_list(dtype), p, bc, kModelCus);
+  const int bc = auto_bc_s5(p, dtype, kModelCus);
+  const int br = auto_br_s5(s5_list(dtype), p, dtype, bc, kModelCus);
   const double cus = static_cast<double>(kModelCus);
   const long long n_qt = (p.N + br - 1) / br;
   const long long longest = (p.N + bc - 1) / bc;
@@ -471,10 +485,11 @@ int forward(int dtype, const void* q, const void* k, const void* v, void* o, flo
   const int rc = common_stage_checks("stage5", q, k, v, o, lse, p);
   if (rc != 0) return rc;
   const VariantList list = s5_list(dtype);
-  int bc = dbg.block_n != 0 ? dbg.block_n : auto_bc_s5(p, current_device_cus());
+  int bc = dbg.block_n != 0 ? dbg.block_n : auto_bc_s5(p, dtype, current_device_cus());
   if (dbg.block_m != 0 && dbg.block_n == 0) bc = width_for_forced_height(list, p.D, dbg.block_m, bc);
   KArgs a = make_args(q, k, v, o, lse, p, st);
-  const int br = dbg.block_m != 0 ? dbg.block_m : auto_br_s5(list, p, bc, current_device_cus());
+  const int br =
+      dbg.block_m != 0 ? dbg.block_m : auto_br_s5(list, p, dtype, bc, current_device_cus());
   // With a workspace (fa_workspace_bytes > 0) the key walks may be split; without one the
   // whole-walk kernel runs.
   const int splits = workspace != nullptr ? s5_splits(p, dtype) : 1;

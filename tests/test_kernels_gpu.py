@@ -130,8 +130,9 @@ def test_stage5_default_height_matches_forced_heights(b, h, n, d, dtype, causal,
     (1, 16, 8192, 128, torch.bfloat16, True, (128, 32)),    # LONG: causal, 4 per CU
     (2, 8, 2048, 64, torch.float16, True, (64, 128)),       # C64 causal: halved height
     (2, 8, 2048, 128, torch.float16, True, (64, 64)),       # C128 causal: halved height
+    (2, 8, 4096, 64, torch.float16, False, (128, 128)),     # D = 64 long walks, 2 per CU: wide
 ], ids=["d64-large", "d128-dense", "d128-short-causal", "d128-causal-2cu", "d128-causal-3cu",
-        "long", "c64-causal", "c128-causal"])
+        "long", "c64-causal", "c128-causal", "d64-long-walk"])
 def test_stage5_automatic_tile_on_full_grids(b, h, n, d, dtype, causal, tile, make_qkv,
                                              reset_overrides):
     require(5, dtype, d)
