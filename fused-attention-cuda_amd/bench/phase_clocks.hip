@@ -73,7 +73,10 @@ __global__ void fill(T* p, size_t n, uint32_t seed, float scale) {
 
 void run(const Shape& s, int launches) {
   const size_t n = static_cast<size_t>(s.B) * s.H * s.N * s.D;
-  constexpr int kSets = 4;
+  // Rotating input sets: 4 (they stay in the 256 MB last-level cache), or PHASE_CLOCKS_SETS of
+  // them, e.g. 32 at C64 (537 MB, twice that cache, as bench.py's cache-cold headline).
+  const char* sets_env = std::getenv("PHASE_CLOCKS_SETS");
+  const int kSets = sets_env != nullptr ? std::max(1, std::min(64, std::atoi(sets_env))) : 4;
   std::vector<void*> q(kSets), k(kSets), v(kSets), o(kSets);
   std::vector<float*> lse(kSets);
   for (int i = 0; i < kSets; ++i) {
@@ -156,9 +159,9 @@ void run(const Shape& s, int launches) {
     return;
   }
   const double flops = 4.0 * s.B * s.H * static_cast<double>(s.N) * s.N * s.D / (s.causal ? 2 : 1);
-  std::printf("%s (B%d H%d N%d D%d %s%s, BR %d x BC %d, %d workgroups x %d waves):\n", s.name,
-              s.B, s.H, s.N, s.D, s.bf16 ? "bf16" : "fp16", s.causal ? " causal" : "", s.br, s.bc,
-              nwg, s.waves);
+  std::printf("%s (B%d H%d N%d D%d %s%s, BR %d x BC %d, %d workgroups x %d waves, %d input sets):\n",
+              s.name, s.B, s.H, s.N, s.D, s.bf16 ? "bf16" : "fp16", s.causal ? " causal" : "", s.br,
+              s.bc, nwg, s.waves, kSets);
   std::printf("  launch (back to back, %d launches): %.2f us, %.1f TFLOP/s = %.1f %% of 2.5 PFLOP/s\n",
               launches, us, flops / us * 1e-6, flops / us * 1e-6 / 25.0);
   std::printf("  shader clock %.2f GHz; workgroup lifetime %.2f us; span first start -> last end "
