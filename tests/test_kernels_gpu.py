@@ -131,8 +131,10 @@ def test_stage5_default_height_matches_forced_heights(b, h, n, d, dtype, causal,
     (2, 8, 2048, 64, torch.float16, True, (64, 128)),       # C64 causal: halved height
     (2, 8, 2048, 128, torch.float16, True, (64, 64)),       # C128 causal: halved height
     (2, 8, 4096, 64, torch.float16, False, (128, 128)),     # D = 64 long walks, 2 per CU: wide
+    (8, 8, 2048, 64, torch.float16, False, (128, 128)),     # 4 per CU, fp16: wide
+    (8, 8, 2048, 64, torch.bfloat16, False, (64, 64)),      # same grid, bf16 keeps narrow
 ], ids=["d64-large", "d128-dense", "d128-short-causal", "d128-causal-2cu", "d128-causal-3cu",
-        "long", "c64-causal", "c128-causal", "d64-long-walk"])
+        "long", "c64-causal", "c128-causal", "d64-long-walk", "d64-fp16-wide", "d64-bf16-narrow"])
 def test_stage5_automatic_tile_on_full_grids(b, h, n, d, dtype, causal, tile, make_qkv,
                                              reset_overrides):
     require(5, dtype, d)
