@@ -189,7 +189,7 @@ struct Dec16 {
       }
       ws.m = m_new;
     }
-    const float lt = ws.l + __shfl_xor(ws.l, 32);
+    const float lt = halves_sum(ws.l);
     if (!row_valid) return;
     const bool empty = !(lt > 0.f) || ws.m == -__builtin_inff();
     const float inv = empty ? 0.f : 1.f / lt;

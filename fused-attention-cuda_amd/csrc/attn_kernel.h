@@ -45,6 +45,7 @@
 #include <type_traits>
 
 #include "fa_internal.h"
+#include "wave_halves.h"
 
 namespace fa {
 namespace kern {
@@ -272,7 +273,7 @@ struct Attn {
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
       }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = halves_max(mx);
     // The reference recurrence moves m to the row max on every tile and rescales acc and l by
     // alpha = exp2((m_old - m_new) c). Here m moves only when some row of the wave sees a max
     // more than kLazyLog2 (exp2 units) above its current m; otherwise p = exp2(s c - m c)
@@ -403,7 +404,7 @@ struct Attn {
     }
 
     // ---- epilogue: O = acc / l, lse = m*scale + ln l (ref:include/fa/softmax_math.cuh:58-71) --
-    const float lt = ws.l + __shfl_xor(ws.l, 32);
+    const float lt = halves_sum(ws.l);
     if (!wave_valid) return;
     const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
     Tio* orow = static_cast<Tio*>(a.o) + b * a.osb + h * a.osh + row * a.osn;

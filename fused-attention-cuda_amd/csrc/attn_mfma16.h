@@ -59,6 +59,7 @@
 #include <type_traits>
 
 #include "fa_internal.h"
+#include "wave_halves.h"
 #include "tile_layout.h"
 
 namespace fa {
@@ -338,8 +339,8 @@ struct Fa16 {
   }
 
   // The row max of a tile: the lane's own 16 (32, 64) scores, then the other half of the row (lane
-  // l ^ 32) through v_permlane32_swap, a VALU exchange of the wave's two 32-lane halves, instead
-  // of an LDS bpermute round trip (measured: LONG, bf16, -1.5 to -2 %; bit-identical).
+  // l ^ 32) through halves_max, a VALU exchange of the wave's two 32-lane halves, instead of an
+  // LDS bpermute round trip (measured: LONG, bf16, -1.5 to -2 %; bit-identical).
   template <bool FULL>
   __device__ static float tile_max(const f32x16 (&s)[kKB], int nvalid) {
     float mx = -__builtin_inff();
@@ -350,11 +351,7 @@ struct Fa16 {
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
       }
     }
-    const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, mx),
-                                                     __builtin_bit_cast(unsigned, mx), false, false);
-    // sw[0] holds the low half's value in both halves, sw[1] the high half's.
-    return fmaxf(__builtin_bit_cast(float, static_cast<unsigned>(sw[0])),
-                 __builtin_bit_cast(float, static_cast<unsigned>(sw[1])));
+    return halves_max(mx);
   }
 
   // Moves the reference max to max(m, mx) and rescales l and O by alpha = exp2((m_old - m_new) c).
@@ -858,7 +855,7 @@ struct Fa16 {
     }
 
     // ---- epilogue: O = acc / l, lse = m*scale + ln l (ref:include/fa/softmax_math.cuh:58-71) ----
-    const float lt = ws.l + __shfl_xor(ws.l, 32);
+    const float lt = halves_sum(ws.l);
     if (!wave_valid) {
       clk_store();
       return;
