@@ -3,9 +3,9 @@
 # ref:scripts/profile.sh, which runs Nsight Compute on the reference's fa_bench).
 #
 #   usage: profile.sh <stage> <cfg> <dtype> <outdir> [causal] [bench-workload]
-#   e.g.   profile.sh 5 C64 fp16 gpurun_out/prof_s5_C64
-#          FA_FORCE_BR=64 FA_FORCE_BC=64 profile.sh 5 B8_H12_N1024_D64 fp16 gpurun_out/gpt_narrow 1
-#          profile.sh 5 C64 fp16 gpurun_out/headline 0 C64      # bench.py --only --workload C64
+#   e.g.   profile.sh 5 C64 fp16 prof/s5_C64
+#          FA_FORCE_BR=64 FA_FORCE_BC=64 profile.sh 5 B8_H12_N1024_D64 fp16 prof/gpt_narrow 1
+#          profile.sh 5 C64 fp16 prof/headline 0 C64      # bench.py --only --workload C64
 #
 # The program profiled is the torch-free fa_bench, launches back to back over 4 rotating input
 # sets (FA_BENCH_FLUSH=1: a 1 GiB flush before every launch, the reference's protocol, whose
