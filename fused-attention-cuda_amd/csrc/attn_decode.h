@@ -106,6 +106,14 @@ struct Dec16 {
     // Last visible key of this lane's row, relative to k_begin.
     const int tok = row % a.Nq;
     const int lim = (a.causal ? a.Nkv - a.Nq + tok : a.Nkv - 1) - k_begin;
+    // bf16 probabilities round to 8 significant bits before the P V MFMA. Over a row's visible
+    // keys those rounding errors average out; over a few of them they do not (a flat row over 6
+    // keys errs by up to 2.4e-3 of |V|). When some row sees fewer than kDecLoKeys keys, every
+    // block therefore also carries its probabilities' low parts (P = hi + lo, exact to ~2^-16),
+    // as the forward kernel does on its causal diagonal. Wave-uniform; long caches never pay it.
+    constexpr int kDecLoKeys = 128;
+    const int min_visible = a.causal ? a.Nkv - a.Nq + 1 : a.Nkv;
+    const int lo_blk = (!F::kF16 && min_visible < kDecLoKeys) ? 0 : -1;
 
     const T* kg = static_cast<const T*>(a.k) + static_cast<size_t>(b * a.Hkv + hkv) * a.Nkv * D +
                   static_cast<size_t>(k_begin) * D;
@@ -149,9 +157,9 @@ struct Dec16 {
           }
         }
         float mx = 0.f;
-        const float rs = F::template softmax_exp<false>(ws, sc, P, mx, nv, -1, c, lane);
-        F::template softmax_settle<false>(ws, sc, P, rs, mx, nv, -1, c);
-        F::template pv<false>(ws, P, vs, vl, nv, -1);
+        const float rs = F::template softmax_exp<false>(ws, sc, P, mx, nv, -1, c, lane, lo_blk);
+        F::template softmax_settle<false>(ws, sc, P, rs, mx, nv, lo_blk, c);
+        F::template pv<false>(ws, P, vs, vl, nv, lo_blk);
       }
       F::wait_dma();
       __syncthreads();

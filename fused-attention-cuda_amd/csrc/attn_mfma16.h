@@ -414,9 +414,13 @@ struct Fa16 {
   //           largest probability would dominate the error of concentrated rows).
   // acc, l and lse all refer to the same m and m only moves to an observed max, so the result is
   // the reference's recurrence. The decision is one ballot (a scalar branch).
+  // `lo` names the block whose bf16 probabilities also get their low parts: the causal diagonal
+  // block by default (kLoAtDiag); the decode passes its own choice with diag = -1 (no mask).
+  static constexpr int kLoAtDiag = -2;
   template <bool FULL>
   __device__ static float softmax_exp(WaveState& ws, f32x16 (&s)[kKB], Probs& P, float& mx,
-                                      int nvalid, int diag, float c, int lane) {
+                                      int nvalid, int diag, float c, int lane,
+                                      int lo = kLoAtDiag) {
     if (!FULL && diag >= 0) {
       const int g = lane >> 5;
 #pragma unroll
@@ -432,7 +436,7 @@ struct Fa16 {
       }
     }
     if constexpr (!kF16) mx = tile_max<FULL>(s, nvalid);
-    return exp_pack<FULL>(s, P, ws, nvalid, diag, c);
+    return exp_pack<FULL>(s, P, ws, nvalid, lo == kLoAtDiag ? diag : lo, c);
   }
 
   template <bool FULL>

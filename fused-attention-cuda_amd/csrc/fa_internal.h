@@ -101,7 +101,7 @@ struct DecArgs {
   int G;      // H / Hkv
   int Nq;
   int Nkv;
-  int R;      // G * Nq query rows per kv head, <= 32
+  int R;      // G * Nq query rows per kv head, <= 64
   int S;      // splits of the key range
   int chunk;  // keys per split, a multiple of the 128-key tile
   float scale;

@@ -8,6 +8,8 @@ the full 32-row group, one split against many, and rows that see no key (Nq > Nk
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -86,6 +88,21 @@ def test_one_split_and_many_splits_agree(dtype):
         assert_close_tol(o, o1.double().cpu().numpy(), atol, rtol)
         assert_close_tol(lse, l1.double().cpu().numpy(), LSE_ATOL, 0.0, what="LSE")
     check(o8, l8, q, k, v, True, dtype)
+
+
+@pytest.mark.parametrize("nkv,nq,causal", [(2, 1, False), (6, 2, False), (16, 4, True),
+                                            (100, 1, False), (140, 16, True), (200, 1, False)])
+def test_bf16_short_cache_flat_rows(nkv, nq, causal):
+    """bf16 rows over a few keys with a small scale (flat probabilities): the probabilities' bf16
+    rounding does not average out over a few keys, so below 128 visible keys the kernel adds their
+    low parts; at and above it (140 keys minus 15 for the first causal token, 200) it does not
+    need them. Both sides must meet the bar."""
+    require_ext()
+    q, k, v = make(2, 8, 4, nq, nkv, 128, torch.bfloat16, seed=11 * nkv + nq)
+    scale = 0.25 / math.sqrt(128)
+    o, lse = fused_attn.decode(q, k, v, is_causal=causal, scale=scale)
+    torch.cuda.synchronize()
+    check(o, lse, q, k, v, causal, torch.bfloat16, scale=scale)
 
 
 def test_rows_without_keys():
