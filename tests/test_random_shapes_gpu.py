@@ -8,7 +8,9 @@
 * fp16 or bf16, causal or not;
 * for some, a forced split count of 2, 3 or 5, with the workspace the op sizes through
   ``fa_workspace_bytes``.
-Each case runs on the tile the library picks by itself. Every head is checked against the fp64
+A second draw of 24 cases takes a softmax scale other than 1/sqrt(D): a quarter of it (flat
+rows, where the 16-bit rounding of the probabilities averages out least) or twice it (peaked
+rows, where the running max moves most). Each case runs on the tile the library picks by itself. Every head is checked against the fp64
 oracle at the stated tolerance (tests/_checks.py). The test id spells out the draw, so a failure
 names its shape.
 """
@@ -44,6 +46,23 @@ def _draw(count: int = 48, seed: int = 20261202):
     return cases
 
 
+def _draw_scaled(count: int = 24, seed: int = 20261204):
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(count):
+        b = rng.choice([1, 2])
+        h = rng.choice([1, 2, 4, 8])
+        hkv = rng.choice([x for x in range(1, h + 1) if h % x == 0])
+        n = 32 * rng.choice([1, 1, 2, 3, rng.randint(4, 16)])
+        d = rng.choice([64, 128])
+        dt = rng.choice(sorted(DTYPES))
+        causal = rng.random() < 0.5
+        splits = rng.choice([0, 0, 2, 3])
+        mul = rng.choice([0.25, 2.0])
+        cases.append((b, h, hkv, n, d, dt, causal, splits, mul))
+    return cases
+
+
 def _case_id(c):
     b, h, hkv, n, d, dt, causal, splits = c
     return f"B{b}H{h}kv{hkv}N{n}D{d}{dt}{'-causal' if causal else ''}{f'-S{splits}' if splits else ''}"
@@ -65,3 +84,23 @@ def test_random_shape_matches_oracle(case, make_qkv, monkeypatch):
     o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
     torch.cuda.synchronize()
     check_against_reference(o, q, k, v, causal, dtype, lse=lse)
+
+
+@pytest.mark.parametrize("case", _draw_scaled(),
+                         ids=lambda c: f"{_case_id(c[:8])}-scale{c[8]}x")
+def test_random_scaled_shape_matches_oracle(case, make_qkv, monkeypatch):
+    if not fused_attn.is_available():
+        pytest.fail("fused_attn._C is not built: the HIP path must be the one that runs")
+    b, h, hkv, n, d, dt, causal, splits, mul = case
+    dtype = DTYPES[dt]
+    if not fused_attn.impl_supports(5, dtype, d):
+        pytest.skip(f"stage 5 is not built for {dt} D={d} on this GPU")
+    if splits:
+        monkeypatch.setenv("FA_FORCE_SPLITS", str(splits))
+    else:
+        monkeypatch.delenv("FA_FORCE_SPLITS", raising=False)
+    q, k, v = make_qkv(b, h, n, d, dtype=dtype, device="cuda", hkv=hkv, seed=n + 5 * h + d + 1)
+    scale = mul / d ** 0.5
+    o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal, scale=scale)
+    torch.cuda.synchronize()
+    check_against_reference(o, q, k, v, causal, dtype, scale=scale, lse=lse)
