@@ -8,6 +8,9 @@
 * fp16 or bf16, causal or not;
 * for some, a forced split count of 2, 3 or 5, with the workspace the op sizes through
   ``fa_workspace_bytes``.
+A third draw of 24 cases runs the other two stages the library builds: stage 3 (the fp32
+rung, checked at fp32's 1e-5 bar) and stage 4 (16-bit, synchronous staging), with GQA, partial
+tiles, D and causal drawn as above.
 A second draw of 24 cases takes a softmax scale other than 1/sqrt(D): a quarter of it (flat
 rows, where the 16-bit rounding of the probabilities averages out least) or twice it (peaked
 rows, where the running max moves most). Each case runs on the tile the library picks by itself. Every head is checked against the fp64
@@ -104,3 +107,34 @@ def test_random_scaled_shape_matches_oracle(case, make_qkv, monkeypatch):
     o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal, scale=scale)
     torch.cuda.synchronize()
     check_against_reference(o, q, k, v, causal, dtype, scale=scale, lse=lse)
+
+
+def _draw_stages(count: int = 24, seed: int = 20261205):
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(count):
+        stage = rng.choice([3, 4])
+        b = rng.choice([1, 2])
+        h = rng.choice([1, 2, 3, 4, 6, 8])
+        hkv = rng.choice([x for x in range(1, h + 1) if h % x == 0])
+        n = 32 * rng.randint(1, 12)
+        d = rng.choice([64, 128])
+        dt = "fp32" if stage == 3 else rng.choice(sorted(DTYPES))
+        causal = rng.random() < 0.5
+        cases.append((stage, b, h, hkv, n, d, dt, causal))
+    return cases
+
+
+@pytest.mark.parametrize("case", _draw_stages(),
+                         ids=lambda c: f"s{c[0]}-{_case_id(c[1:] + (0,))}")
+def test_random_shape_other_stages(case, make_qkv):
+    if not fused_attn.is_available():
+        pytest.fail("fused_attn._C is not built: the HIP path must be the one that runs")
+    stage, b, h, hkv, n, d, dt, causal = case
+    dtype = torch.float32 if dt == "fp32" else DTYPES[dt]
+    if not fused_attn.impl_supports(stage, dtype, d):
+        pytest.skip(f"stage {stage} is not built for {dt} D={d} on this GPU")
+    q, k, v = make_qkv(b, h, n, d, dtype=dtype, device="cuda", hkv=hkv, seed=n + 3 * h + d + stage)
+    o, lse = fused_attn.forward_stage(q, k, v, stage, is_causal=causal)
+    torch.cuda.synchronize()
+    check_against_reference(o, q, k, v, causal, dtype, lse=lse)
