@@ -5,6 +5,8 @@ the fp64 oracle. The output of ``forward_strided`` is dense in q's memory order.
 
 from __future__ import annotations
 
+import random
+
 import pytest
 import torch
 
@@ -103,3 +105,58 @@ def test_opcheck_forward_strided():
     q, k, v = qkv_views(1, 2, 2, 128, 64, torch.float16, seed=11)
     torch.library.opcheck(torch.ops.fused_attn.forward_strided, (q, k, v, True, 0.125),
                           test_utils=("test_schema", "test_faketensor"))
+
+
+def _layout_views(layout, b, h, hkv, n, d, dtype, seed):
+    """q, k, v [B, *, N, D] views of one of three memory layouts (each row 16-byte aligned):
+    'qkv' the fused projection buffer above; 'padded' [B, N, heads, D + pad] buffers cut to D;
+    'batch' every other batch of [2B, heads, N, D] buffers (a doubled batch stride)."""
+    if layout == "qkv":
+        return qkv_views(b, h, hkv, n, d, dtype, seed)
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    pad = 16 // torch.empty((), dtype=dtype).element_size() * (1 + seed % 3)
+    out = []
+    for heads in (h, hkv, hkv):
+        if layout == "padded":
+            buf = torch.randn(b, n, heads, d + pad, generator=gen).to("cuda", dtype)
+            out.append(buf[..., :d].transpose(1, 2))
+        else:
+            buf = torch.randn(2 * b, heads, n, d, generator=gen).to("cuda", dtype)
+            out.append(buf[::2])
+    return tuple(out)
+
+
+def _draw_strided(count: int = 24, seed: int = 20261206):
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(count):
+        layout = rng.choice(["qkv", "padded", "batch"])
+        b = rng.choice([1, 2, 3])
+        h = rng.choice([1, 2, 4, 6, 8])
+        hkv = rng.choice([x for x in range(1, h + 1) if h % x == 0])
+        n = 32 * rng.randint(1, 12)
+        d = rng.choice([64, 128])
+        dtype = rng.choice(DTYPES)
+        causal = rng.random() < 0.5
+        cases.append((layout, b, h, hkv, n, d, dtype, causal))
+    return cases
+
+
+@pytest.mark.parametrize("case", _draw_strided(), ids=lambda c: "{}-B{}H{}kv{}N{}D{}{}{}".format(
+    c[0], *c[1:6], _ids[c[6]], "-causal" if c[7] else ""))
+def test_random_strided_layouts(case):
+    """Seeded random layouts, shapes, dtypes and masks: forward_strided on the views equals the
+    dense forward on the same data bit for bit, and that forward meets the bar against the fp64
+    oracle."""
+    require_ext()
+    layout, b, h, hkv, n, d, dtype, causal = case
+    q, k, v = _layout_views(layout, b, h, hkv, n, d, dtype, seed=n + h + d)
+    assert q.stride(-1) == 1
+    assert not q.is_contiguous() or (layout == "batch" and b == 1)  # one batch of B is dense
+    print(f"strided case {case}", flush=True)
+    o = fused_attn.forward_strided(q, k, v, is_causal=causal)
+    qd, kd, vd = q.contiguous(), k.contiguous(), v.contiguous()
+    o_dense = fused_attn.forward(qd, kd, vd, is_causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_dense)
+    check_against_reference(o_dense, qd, kd, vd, causal, dtype)
