@@ -11,6 +11,8 @@
 A third draw of 24 cases runs the other two stages the library builds: stage 3 (the fp32
 rung, checked at fp32's 1e-5 bar) and stage 4 (16-bit, synchronous staging), with GQA, partial
 tiles, D and causal drawn as above.
+A fourth draw of 12 cases takes sequences of 640 to 4096 tokens, checked on every head
+against plain PyTorch fp32 attention on the GPU (the fp64 oracle would take minutes there).
 A second draw of 24 cases takes a softmax scale other than 1/sqrt(D): a quarter of it (flat
 rows, where the 16-bit rounding of the probabilities averages out least) or twice it (peaked
 rows, where the running max moves most). Each case runs on the tile the library picks by itself. Every head is checked against the fp64
@@ -26,7 +28,7 @@ import pytest
 import torch
 
 import fused_attn
-from _checks import check_against_reference
+from _checks import LSE_ATOL, O_TOL, check_against_reference, fp32_reference_head
 
 pytestmark = pytest.mark.gpu
 
@@ -138,3 +140,44 @@ def test_random_shape_other_stages(case, make_qkv):
     o, lse = fused_attn.forward_stage(q, k, v, stage, is_causal=causal)
     torch.cuda.synchronize()
     check_against_reference(o, q, k, v, causal, dtype, lse=lse)
+
+
+def _draw_large(count: int = 12, seed: int = 20261207):
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(count):
+        b = rng.choice([1, 2, 4])
+        h = rng.choice([2, 4, 8, 12, 16])
+        hkv = rng.choice([x for x in range(1, h + 1) if h % x == 0])
+        n = 32 * rng.randint(20, 128)
+        d = rng.choice([64, 128])
+        dt = rng.choice(sorted(DTYPES))
+        causal = rng.random() < 0.5
+        cases.append((b, h, hkv, n, d, dt, causal, 0))
+    return cases
+
+
+@pytest.mark.parametrize("case", _draw_large(), ids=lambda c: f"large-{_case_id(c)}")
+def test_random_large_shape_every_head(case, make_qkv, monkeypatch):
+    """Sequences of 640 to 4096 tokens (the automatic tile and split choices of mid-sized grids),
+    every row of every head against plain PyTorch fp32 attention on the GPU at the stated bar."""
+    if not fused_attn.is_available():
+        pytest.fail("fused_attn._C is not built: the HIP path must be the one that runs")
+    b, h, hkv, n, d, dt, causal, _ = case
+    dtype = DTYPES[dt]
+    if not fused_attn.impl_supports(5, dtype, d):
+        pytest.skip(f"stage 5 is not built for {dt} D={d} on this GPU")
+    monkeypatch.delenv("FA_FORCE_SPLITS", raising=False)
+    q, k, v = make_qkv(b, h, n, d, dtype=dtype, device="cuda", hkv=hkv, seed=n + h + d + 2)
+    scale = 1.0 / d ** 0.5
+    o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
+    torch.cuda.synchronize()
+    atol, rtol = O_TOL[dtype]
+    for bi in range(b):
+        for hi in range(h):
+            o32, lse32, _s = fp32_reference_head(q, k, v, bi, hi, causal, scale)
+            err = (o[bi, hi].float() - o32).abs()
+            excess = float((err - (atol + rtol * o32.abs())).max())
+            assert excess <= 0.0, f"head ({bi},{hi}): max|O err| {float(err.max()):.3e}"
+            lerr = float((lse[bi, hi] - lse32).abs().max())
+            assert lerr <= LSE_ATOL, f"head ({bi},{hi}): max|LSE err| {lerr:.3e}"
