@@ -145,13 +145,17 @@ def gate(torch, capi, q, k, v, o, lse, causal, scale, stage, stream):
     return worst_o, worst_l
 
 
-def time_steps(torch, capi, args_list, causal, scale, stage, stream, steps, warmup):
+def time_steps(torch, capi, args_list, causal, scale, stage, stream, steps, warmup, repeats=1,
+               min_warm_s=0.0):
     """Warmup, then K launches bracketed by events on the launch stream; average ms per launch
-    (None when K is 0: warm-up only).
+    (None when K is 0: warm-up only), or with ``repeats`` = 3 the median of three such loops.
     args_list rotates over input sets (q, k, v, o, lse). The fa_forward arguments of each set are
     marshalled once, so the timed loop is one C call per launch and the host stays ahead of the
-    GPU."""
+    GPU. ``min_warm_s`` extends the warm-up to at least that many seconds of launches: a timed
+    loop that starts while the GPU is still coming out of an idle spell (a CPU-side gate just ran)
+    otherwise reads short kernels at up to twice their time."""
     import ctypes
+    import time
 
     lib = capi.load()
     calls = []
@@ -171,16 +175,24 @@ def time_steps(torch, capi, args_list, causal, scale, stage, stream, steps, warm
 
     for i in range(warmup):
         launch(calls[i % len(calls)])
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < min_warm_s:
+        for c in calls:
+            launch(c)
+        stream.synchronize()
     stream.synchronize()
     if steps == 0:
         return None
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(steps):
-        launch(calls[i % len(calls)])
-    end.record(stream)
-    end.synchronize()
-    return start.elapsed_time(end) / steps
+    times = []
+    for _ in range(repeats):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(steps):
+            launch(calls[i % len(calls)])
+        end.record(stream)
+        end.synchronize()
+        times.append(start.elapsed_time(end) / steps)
+    return sorted(times)[len(times) // 2]
 
 
 def graph_timing(torch, capi, args_list, causal, scale, stage, stream, steps, repeats=1):
@@ -356,7 +368,8 @@ def bench_workload(torch, capi, name, stage, steps, warmup, seed=0, gate_it=True
     stream.synchronize()
     err = gate(torch, capi, *sets[0], causal, scale, stage, stream) if gate_it else (None, None)
     eager_ms = time_steps(torch, capi, sets, causal, scale, stage, stream,
-                          steps if eager else 0, warmup)
+                          steps if eager else 0, warmup, repeats=3,
+                          min_warm_s=0.05 if eager else 0.0)
     ms = (graph_timing(torch, capi, sets, causal, scale, stage, stream, steps, repeats=3)
           if replay else None)
     f = flops(b, h, n, d, causal)
@@ -610,7 +623,8 @@ def main(argv=None) -> int:
                                   "tflops": round(etf, 3),
                                   "pct_of_peak": round(100.0 * etf / PEAK_TFLOPS[dt], 3),
                                   "what": "the same K launches issued one by one from the host "
-                                          "(ctypes -> fa_forward), one event pair around the loop"}
+                                          "(ctypes -> fa_forward) after a 50 ms warm-up, one event pair "
+                                          "around each loop, the median of three loops"}
     if vendor is not None:
         line["vendor_sdpa"] = {"ms": round(vendor, 6),
                                "fused_speedup_eager": round(vendor / head["eager_ms"], 3),
