@@ -108,7 +108,7 @@ struct Dec16 {
     const int lim = (a.causal ? a.Nkv - a.Nq + tok : a.Nkv - 1) - k_begin;
     // bf16 probabilities round to 8 significant bits before the P V MFMA. Over a row's visible
     // keys those rounding errors average out; over a few of them they do not (a flat row over 6
-    // keys errs by up to 2.4e-3 of |V|). When some row sees fewer than kDecLoKeys keys, every
+    // keys of unit-variance V errs by up to 2.4e-3). When some row sees fewer than kDecLoKeys keys, every
     // block therefore also carries its probabilities' low parts (P = hi + lo, exact to ~2^-16),
     // as the forward kernel does on its causal diagonal. Wave-uniform; long caches never pay it.
     constexpr int kDecLoKeys = 128;
