@@ -7,9 +7,9 @@ non-causal, through the stage-5 kernel (``fa_s5_tuned``, what ``torch.ops.fused_
 dispatches to for fp16). A *step* is one forward over one batch of synthetic inputs resident in
 HBM. The kernel is launched through the C-ABI (``fa_forward`` of libfa_hip.so) on a dedicated HIP
 stream. The K timed steps are K launches issued back to back from the host, after a 50 ms
-warm-up, bracketed by HIP events recorded on that same stream. They rotate over input sets that
-together are twice the 256 MB last-level cache, so every launch reads its inputs from HBM
-(``value``). The same launches captured once into a HIP graph and replayed over the same sets
+warm-up, bracketed by HIP events recorded on that same stream; the loop runs three times and the
+median is ``value``. They rotate over input sets that together are twice the 256 MB last-level
+cache, so every launch reads its inputs from HBM. The same launches captured once into a HIP graph and replayed over the same sets
 (``graph_replay``; every output of two checked replays is compared bitwise with eager launches
 first), the graph replay over 4 sets that stay cache-resident (``warm_replay``), eager launches
 over those 4 sets (``eager_launches``) and the reference's protocol (``protocol``, a 1 GiB flush
@@ -23,12 +23,14 @@ Printed: ONE JSON line with the contract fields, plus
   kind "reference"; the C restatement, kind "port", when _ref is absent) timed on the host cores
   over the same workload, repeated for a bounded budget of CPU time;
 * ``cpu_baseline``'s ``single_thread``: the same oracle on one thread, the reference's own loops;
-* ``configs``: the other benchmark configurations (C128, C128 causal, the long-context shape LONG
-  with its N sweep 512 / 1024 / 4096 / 8192, the GPT-2 attention shape; the fp32 rung, stage 3,
-  at BASELINE configs[0] -- timed beside the reference's CPU oracle on that whole workload -- and
-  at C64 against the fp32 MFMA roof), each with ms and TFLOP/s of the 4-set graph replay and
-  ``eager_ms``, plus one GPU's share of 8-GPU layouts (C64 and LONG split over heads, one ring
-  step of LONG split over the sequence);
+* ``configs``: the other benchmark configurations (C128, C64 and C128 causal, the long-context
+  shape LONG with its N sweep 512 / 1024 / 4096 / 8192, the GPT-2 attention shape; the fp32
+  rung, stage 3, at BASELINE configs[0] -- timed beside the reference's CPU oracle on that whole
+  workload -- and at C64 and C128 against the fp32 MFMA roof; stage 4 at C64 and C128), each
+  timed like ``value`` (``ms``: host-issued launches over cache-cold sets, median of three) and
+  over 4 cache-resident sets (``warm_ms``), plus one GPU's share of 8-GPU layouts (C64 and LONG
+  split over heads, one ring step of LONG split over the sequence);
+* ``causal_speedup``: dense over causal time at C64 and C128 (tile skipping; 2x is the ideal);
 * ``vendor_sdpa``: torch's ``scaled_dot_product_attention`` on the same inputs (fp16 configs);
 * ``protocol``: the reference's timing protocol (ref:docs/BENCHMARK_PROTOCOL.md rules 1-2) on the
   headline workload: 1 GiB flush before every launch, one event pair per launch, median/p10/p90.
@@ -75,7 +77,23 @@ WORKLOADS = {
     "C64_heads8": (2, 1, 2048, 64, "fp16", False, 1.0),
     "LONG_heads8": (1, 2, 8192, 128, "bf16", True, 0.5),
     "LONG_ring8": (1, 16, 1024, 128, "bf16", False, 0.5),
+    # Causal C64, for the causal-over-dense ratio at both head dims (the reference publishes its
+    # tile-skipping speedup, ref:docs/STAGES.md:644-652).
+    "C64_causal": (2, 8, 2048, 64, "fp16", True, 1.0),
+    # The rest of the reference's ladder at the canonical shapes (ref:bench/results/t4/
+    # summary.csv:393, :445, :452): stage 4 (the synchronous loop) at C64 and C128, and the fp32
+    # rung (stage 3) at C128.
+    "C64_s4": (2, 8, 2048, 64, "fp16", False, 1.0),
+    "C128_s4": (2, 8, 2048, 128, "fp16", False, 1.0),
+    "C128_fp32": (2, 8, 2048, 128, "fp32", False, 1.0),
 }
+# The stage each workload runs on: stage 3 for fp32 (the fp32 rung), 4 for the stage-4 rows, 5
+# otherwise (what torch.ops.fused_attn.forward dispatches to for fp16 / bf16).
+STAGE_OF = {"C64_s4": 4, "C128_s4": 4}
+
+
+def stage_of(name: str) -> int:
+    return STAGE_OF.get(name, 3 if WORKLOADS[name][4] == "fp32" else 5)
 
 
 def flops(b, h, n, d, causal) -> float:
@@ -245,16 +263,16 @@ def graph_timing(torch, capi, args_list, causal, scale, stage, stream, steps, re
 LLC_BYTES = 256 << 20
 
 
-def cold_timing(torch, capi, name, stage, steps, warmup, graph=True):
+def cold_timing(torch, capi, name, stage, steps, warmup, graph=True, repeats=3):
     """The headline timing: K launches issued back to back from the host over enough rotating
     input sets that together they are twice the last-level cache, so every launch finds its inputs
     in HBM, not in a cache left warm by an earlier launch, and nothing but the kernels runs in the
     timed region (no flush kernel). One event pair brackets exactly K launches, after a 50 ms
-    warm-up and a synchronisation. With ``graph`` the same launches are first captured into a HIP
-    graph and replayed (outputs compared bitwise with eager launches), and that replay's time is
-    returned as well; the eager loop runs last, so that under a profiler the last K dispatches of
-    the trace are the timed ones. Returns (eager ms per launch, graph ms per launch or None,
-    sets)."""
+    warm-up and a synchronisation; the loop runs ``repeats`` times and the median is returned.
+    With ``graph`` the same launches are first captured into a HIP graph and replayed (outputs
+    compared bitwise with eager launches), and that replay's time is returned as well; the eager
+    loops run last, so that under a profiler the last ``repeats`` x K dispatches of the trace are
+    the timed ones. Returns (eager ms per launch, graph ms per launch or None, sets)."""
     b, h, n, d, dt, causal, std = WORKLOADS[name]
     dtype = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[dt]
     esize = 4 if dt == "fp32" else 2
@@ -273,7 +291,7 @@ def cold_timing(torch, capi, name, stage, steps, warmup, graph=True):
     graph_ms = (graph_timing(torch, capi, sets, causal, scale, stage, stream, max(steps, 2 * nsets))
                 if graph else None)
     eager_ms = time_steps(torch, capi, sets, causal, scale, stage, stream, steps, warmup,
-                          min_warm_s=0.05)
+                          repeats=repeats, min_warm_s=0.05)
     del sets
     torch.cuda.empty_cache()
     return eager_ms, graph_ms, nsets
@@ -535,6 +553,9 @@ def main(argv=None) -> int:
     ap.add_argument("--only", action="store_true",
                     help="headline workload only: no other configs, no protocol, no CPU baseline "
                          "(for profiler runs)")
+    ap.add_argument("--with-graph", action="store_true",
+                    help="with --only: also replay the headline launches from a HIP graph before "
+                         "the host-issued loops, so one kernel trace holds both modes")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="CPU seconds (threads x wall) of CPU-baseline work to time")
     ap.add_argument("--grid", action="store_true",
@@ -592,7 +613,7 @@ def main(argv=None) -> int:
     # The headline: K launches issued back to back over input sets that together are twice the
     # last-level cache, so every launch reads its inputs from HBM.
     cold_ms, cold_graph_ms, cold_sets = cold_timing(torch, capi, a.workload, a.stage, a.steps,
-                                                    a.warmup, graph=not a.only)
+                                                    a.warmup, graph=not a.only or a.with_graph)
     achieved = head["flops"] / (cold_ms * 1e-3) / 1e12
     esize = 2 if dt in ("fp16", "bf16") else 4
     vendor = None
@@ -661,24 +682,43 @@ def main(argv=None) -> int:
         for name in WORKLOADS:
             if name == a.workload:
                 continue
-            # Each secondary config gets its own long warm-up: it follows a different workload
-            # (and the CPU baseline's idle GPU), and the clock settles within tens of launches.
-            stage = 3 if WORKLOADS[name][4] == "fp32" else 5  # fp32 runs on the fp32 rung
-            res, s2, st2, c2, sc2 = bench_workload(torch, capi, name, stage,
-                                                   max(50, a.steps // 2), max(50, a.warmup))
+            # Every row is timed like `value`: host-issued launches over cache-cold sets, the
+            # median of three loops (``ms``). Each row first gets its own warm-up (it follows a
+            # different workload, and the CPU baseline's idle GPU), its correctness gate and the
+            # same launches over 4 cache-resident sets (``warm_ms``).
+            stage = stage_of(name)
+            k_row, w_row = max(50, a.steps // 2), max(50, a.warmup)
+            res, s2, st2, c2, sc2 = bench_workload(torch, capi, name, stage, k_row, w_row,
+                                                   replay=False)
+            res["warm_ms"] = res.pop("eager_ms")
             if name == "CPU_cfg":
                 # BASELINE configs[0] is small enough for the reference's CPU oracle to time in
                 # full beside the GPU: the same workload on one host thread.
                 res["cpu_reference"] = cpu_baseline(*s2[0][:3], c2, sc2, s2[0][3], 1.0)
             # Vendor SDPA beside the fp16 configs only: its bf16 fallback path goes through
             # batched products on transposed views, which have faulted on these boxes.
-            if res["dtype"] == "fp16":
-                res["vendor_sdpa_ms"] = sdpa_ms(torch, s2, c2, sc2, st2, max(50, a.steps // 2),
-                                                max(50, a.warmup))
+            if res["dtype"] == "fp16" and stage == 5:
+                res["vendor_sdpa_ms"] = sdpa_ms(torch, s2, c2, sc2, st2, k_row, w_row)
             del s2
+            torch.cuda.empty_cache()
+            cold, _, nsets = cold_timing(torch, capi, name, stage, k_row, w_row, graph=False)
+            tf = res["flops"] / (cold * 1e-3) / 1e12
+            res.update(ms=cold, tflops=tf, pct_peak=100.0 * tf / PEAK_TFLOPS[res["dtype"]],
+                       cold_sets=nsets)
             others[name] = {kk: (round(vv, 6) if isinstance(vv, float) else vv)
                             for kk, vv in res.items()}
         line["configs"] = others
+        line["configs_protocol"] = (
+            "ms: host-issued launches over rotating input sets that together are twice the "
+            "256 MB last-level cache (cold_sets), median of three loops, as `value`; warm_ms: the "
+            "same over 4 cache-resident sets")
+        # Tile skipping: causal over dense time at the two canonical head dims (the reference
+        # reports 1.64-1.86x for its stage 5, ref:docs/STAGES.md:644-652; 2x is the ideal).
+        line["causal_speedup"] = {
+            "C64": round(cold_ms / others["C64_causal"]["ms"], 3)
+            if a.workload == "C64" and "C64_causal" in others else None,
+            "C128": round(others["C128"]["ms"] / others["C128_causal"]["ms"], 3)
+            if "C128" in others and "C128_causal" in others else None}
         line["gpt_block"] = gpt_block_line(torch)
         line["decode"] = decode_line(torch)
     print(json.dumps(line))

@@ -347,79 +347,110 @@ bool emit(const std::vector<std::string>& cols, const std::string& out) {
   return true;
 }
 
-// fp64 attention of query rows [r0, r0 + nr) of one head against all keys (top-left causal),
-// O and LSE = m*scale + ln(sum): the sanity check of this harness.
-void rows_fp64(const std::vector<double>& q, const std::vector<double>& k,
-               const std::vector<double>& v, int N, int D, double scale, bool causal, int r0,
-               int nr, std::vector<double>* o, std::vector<double>* lse) {
-  std::vector<double> s(N);
-  for (int i = 0; i < nr; ++i) {
-    const int row = r0 + i;
-    const int kend = causal ? row + 1 : N;
-    double m = -INFINITY;
-    for (int j = 0; j < kend; ++j) {
-      double d = 0;
-      for (int x = 0; x < D; ++x) d += q[static_cast<std::size_t>(i) * D + x] * k[static_cast<std::size_t>(j) * D + x];
-      s[j] = d * scale;
-      m = std::max(m, s[j]);
-    }
-    double l = 0;
-    for (int j = 0; j < kend; ++j) l += (s[j] = std::exp(s[j] - m));
-    for (int x = 0; x < D; ++x) {
-      double acc = 0;
-      for (int j = 0; j < kend; ++j) acc += s[j] * v[static_cast<std::size_t>(j) * D + x];
-      (*o)[static_cast<std::size_t>(i) * D + x] = acc / l;
-    }
-    (*lse)[i] = m + std::log(l);
-  }
+// ---- the sanity check that gates every row --------------------------------------------------
+// `count` elements of a device tensor from element `first` on, copied to the host and widened.
+std::vector<double> fetch(const void* dev, std::size_t first, std::size_t count, int dt) {
+  const std::size_t width = fa_dtype_size(dt);
+  std::vector<uint8_t> raw(count * width);
+  HIP_OK(hipMemcpy(raw.data(), static_cast<const uint8_t*>(dev) + first * width, raw.size(),
+                   hipMemcpyDeviceToHost));
+  std::vector<double> out(count);
+  for (std::size_t i = 0; i < count; ++i) out[i] = to_double(raw.data(), i, dt);
+  return out;
 }
 
-bool self_check(const fa_params& p, int dt, const void* dq, const void* dk, const void* dv,
-                const void* dO, const float* dlse, int rows, int* checked) {
-  const std::size_t es = fa_dtype_size(dt);
-  const std::size_t nd = static_cast<std::size_t>(p.N) * p.D;
-  std::vector<std::pair<int, int>> ranges;
-  if (p.N <= rows) {
-    ranges.emplace_back(0, p.N);
-  } else {
-    const int half = std::max(1, rows / 2);
-    ranges.emplace_back(0, half);
-    ranges.emplace_back(p.N - half, half);
+// One query row in fp64 against its `visible` keys: the scores' maximum first, then the weights
+// exp(s - max), their sum and the weighted values. Writes the D outputs and the row's LSE
+// (max + ln sum, in the same units as the kernel's: the scale applied).
+void attend_row(const double* qr, const double* keys, const double* vals, int visible, int D,
+                double scale, double* out, double* lse) {
+  std::vector<double> w(visible);
+  double top = -INFINITY;
+  for (int j = 0; j < visible; ++j) {
+    const double* kr = keys + static_cast<std::size_t>(j) * D;
+    double dot = 0;
+    for (int x = 0; x < D; ++x) dot += qr[x] * kr[x];
+    w[j] = dot * scale;
+    top = std::max(top, w[j]);
   }
-  std::vector<std::pair<int, int>> heads = {{0, 0}};
-  if (p.B > 1 || p.H > 1) heads.emplace_back(p.B - 1, p.H - 1);
-  const double cap = dt == FA_DTYPE_F32 ? 1e-4 : dt == FA_DTYPE_F16 ? 1e-2 : 5e-2;
-  double err_o = 0, err_l = 0;
-  *checked = 0;
-  std::vector<uint8_t> hk(nd * es), hv(nd * es);
-  std::vector<double> k(nd), v(nd);
-  for (const auto& [b, h] : heads) {
-    const int hk_idx = h / (p.H / p.Hkv);
-    const std::size_t kv_off = (static_cast<std::size_t>(b) * p.Hkv + hk_idx) * nd * es;
-    HIP_OK(hipMemcpy(hk.data(), static_cast<const uint8_t*>(dk) + kv_off, hk.size(), hipMemcpyDeviceToHost));
-    HIP_OK(hipMemcpy(hv.data(), static_cast<const uint8_t*>(dv) + kv_off, hv.size(), hipMemcpyDeviceToHost));
-    for (std::size_t i = 0; i < nd; ++i) k[i] = to_double(hk.data(), i, dt), v[i] = to_double(hv.data(), i, dt);
-    for (const auto& [r0, nr] : ranges) {
-      const std::size_t rd = static_cast<std::size_t>(nr) * p.D;
-      const std::size_t q_off = ((static_cast<std::size_t>(b) * p.H + h) * p.N + r0) * p.D * es;
-      const std::size_t l_off = (static_cast<std::size_t>(b) * p.H + h) * p.N + r0;
-      std::vector<uint8_t> hq(rd * es), ho(rd * es);
-      std::vector<float> hl(nr);
-      HIP_OK(hipMemcpy(hq.data(), static_cast<const uint8_t*>(dq) + q_off, hq.size(), hipMemcpyDeviceToHost));
-      HIP_OK(hipMemcpy(ho.data(), static_cast<const uint8_t*>(dO) + q_off, ho.size(), hipMemcpyDeviceToHost));
-      HIP_OK(hipMemcpy(hl.data(), dlse + l_off, hl.size() * 4, hipMemcpyDeviceToHost));
-      std::vector<double> q(rd), o_ref(rd), l_ref(nr);
-      for (std::size_t i = 0; i < rd; ++i) q[i] = to_double(hq.data(), i, dt);
-      rows_fp64(q, k, v, p.N, p.D, p.scale, p.causal, r0, nr, &o_ref, &l_ref);
-      for (std::size_t i = 0; i < rd; ++i) err_o = std::max(err_o, std::fabs(to_double(ho.data(), i, dt) - o_ref[i]));
-      for (int i = 0; i < nr; ++i) err_l = std::max(err_l, std::fabs(hl[i] - l_ref[i]));
-      *checked += nr;
+  double total = 0;
+  for (int j = 0; j < visible; ++j) total += (w[j] = std::exp(w[j] - top));
+  for (int x = 0; x < D; ++x) out[x] = 0;
+  for (int j = 0; j < visible; ++j) {
+    const double* vr = vals + static_cast<std::size_t>(j) * D;
+    for (int x = 0; x < D; ++x) out[x] += w[j] * vr[x];
+  }
+  for (int x = 0; x < D; ++x) out[x] /= total;
+  *lse = top + std::log(total);
+}
+
+// A slice of the output the check recomputes: query rows [row0, row0 + nrows) of head (b, h).
+struct Slice {
+  int b, h, row0, nrows;
+};
+
+// The first and the last `rows`/2 query rows (every row when N <= rows) of head (0, 0) and, when
+// there is more than one head, of head (B-1, H-1): the rows and heads the reference's harness
+// checks (ref:bench/bench_main.cu:589-655).
+std::vector<Slice> check_slices(const fa_params& p, int rows) {
+  std::vector<std::pair<int, int>> heads{{0, 0}};
+  if (p.B * p.H > 1) heads.push_back({p.B - 1, p.H - 1});
+  std::vector<Slice> out;
+  for (const auto& bh : heads) {
+    if (p.N <= rows) {
+      out.push_back({bh.first, bh.second, 0, p.N});
+    } else {
+      const int edge = std::max(1, rows / 2);
+      out.push_back({bh.first, bh.second, 0, edge});
+      out.push_back({bh.first, bh.second, p.N - edge, edge});
     }
   }
-  const bool ok = err_o <= cap && err_l <= 10 * cap;
+  return out;
+}
+
+// Recomputes the check slices in fp64 and compares the largest absolute errors with the
+// reference harness's sanity caps: 1e-4 / 1e-2 / 5e-2 on O for fp32 / fp16 / bf16, ten times that
+// on LSE (ref:bench/bench_main.cu:603, :650). Prints one CHECK_OK / CHECK_FAIL line.
+bool self_check(const fa_params& p, int dt, const void* dq, const void* dk, const void* dv,
+                const void* dO, const float* dlse, int rows, int* checked) {
+  const double o_cap = dt == FA_DTYPE_F32 ? 1e-4 : (dt == FA_DTYPE_F16 ? 1e-2 : 5e-2);
+  const std::size_t head_elems = static_cast<std::size_t>(p.N) * p.D;
+  const std::vector<Slice> slices = check_slices(p, rows);
+  double worst_o = 0, worst_lse = 0;
+  int rows_seen = 0, cached_kv = -1;
+  std::vector<double> keys, vals;
+  for (const Slice& sl : slices) {
+    const int kv_head = sl.b * p.Hkv + sl.h / (p.H / p.Hkv);
+    if (kv_head != cached_kv) {
+      keys = fetch(dk, kv_head * head_elems, head_elems, dt);
+      vals = fetch(dv, kv_head * head_elems, head_elems, dt);
+      cached_kv = kv_head;
+    }
+    const std::size_t head_row0 = (static_cast<std::size_t>(sl.b) * p.H + sl.h) * p.N + sl.row0;
+    const std::vector<double> qs = fetch(dq, head_row0 * p.D, sl.nrows * std::size_t(p.D), dt);
+    const std::vector<double> os = fetch(dO, head_row0 * p.D, sl.nrows * std::size_t(p.D), dt);
+    std::vector<float> lse_gpu(sl.nrows);
+    HIP_OK(hipMemcpy(lse_gpu.data(), dlse + head_row0, lse_gpu.size() * sizeof(float),
+                     hipMemcpyDeviceToHost));
+    std::vector<double> expect(p.D);
+    for (int r = 0; r < sl.nrows; ++r) {
+      const int visible = p.causal ? sl.row0 + r + 1 : p.N;
+      double lse64 = 0;
+      attend_row(&qs[static_cast<std::size_t>(r) * p.D], keys.data(), vals.data(), visible, p.D,
+                 p.scale, expect.data(), &lse64);
+      for (int x = 0; x < p.D; ++x) {
+        worst_o = std::max(worst_o, std::fabs(os[static_cast<std::size_t>(r) * p.D + x] - expect[x]));
+      }
+      worst_lse = std::max(worst_lse, std::fabs(static_cast<double>(lse_gpu[r]) - lse64));
+    }
+    rows_seen += sl.nrows;
+  }
+  *checked = rows_seen;
+  const std::size_t heads = slices.size() / (p.N <= rows ? 1 : 2);
+  const bool pass = worst_o <= o_cap && worst_lse <= 10 * o_cap;
   std::printf("%s rows=%d heads=%zu max_abs_err_o=%.3g (cap %.0e) max_abs_err_lse=%.3g\n",
-              ok ? "CHECK_OK" : "CHECK_FAIL", *checked, heads.size(), err_o, cap, err_l);
-  return ok;
+              pass ? "CHECK_OK" : "CHECK_FAIL", rows_seen, heads, worst_o, o_cap, worst_lse);
+  return pass;
 }
 
 int list_support(const DeviceInfo& dev) {
@@ -455,24 +486,27 @@ int run(const Options& opt, const DeviceInfo& dev, hipStream_t stream) {
                 fa_impl_name(opt.stage), fa_dtype_name(dt), p.D, dev.arch);
     return kNotImplemented;
   }
+  // Device memory: every rotating set holds its own q, k and v; O, LSE, the workspace and the
+  // flush buffer are shared by all launches. As many sets as fit in 90 % of the free memory, at
+  // most kMaxSets.
   const std::size_t es = fa_dtype_size(dt);
-  const std::size_t q_bytes = static_cast<std::size_t>(p.B) * p.H * p.N * p.D * es;
-  const std::size_t kv_bytes = static_cast<std::size_t>(p.B) * p.Hkv * p.N * p.D * es;
-  const std::size_t lse_bytes = static_cast<std::size_t>(p.B) * p.H * p.N * sizeof(float);
+  const std::size_t rows_q = static_cast<std::size_t>(p.B) * p.H * p.N;
+  const std::size_t rows_kv = static_cast<std::size_t>(p.B) * p.Hkv * p.N;
+  const std::size_t q_bytes = rows_q * p.D * es;  // also the size of O
+  const std::size_t kv_bytes = rows_kv * p.D * es;
+  const std::size_t lse_bytes = rows_q * sizeof(float);
   const std::size_t ws_bytes = fa_workspace_bytes(opt.stage, dt, &p);
-  const std::size_t set_bytes = q_bytes + 2 * kv_bytes;
-  const std::size_t flush_bytes = opt.flush ? kFlushBytes : 0;
-  const std::size_t fixed = q_bytes + lse_bytes + ws_bytes + flush_bytes;
-  // Rotating input sets: as many as fit (at most kMaxSets) in 90 % of the free memory after the
-  // buffers every launch shares (O, LSE, workspace, the flush buffer).
-  const std::size_t usable = dev.free / 10 * 9;
-  const std::size_t room = usable > fixed ? usable - fixed : 0;
-  if (room < set_bytes) {
+  const std::size_t per_set = q_bytes + 2 * kv_bytes;
+  const std::size_t shared = q_bytes + lse_bytes + ws_bytes + (opt.flush ? kFlushBytes : 0);
+  const std::size_t budget = dev.free - dev.free / 10;
+  const std::size_t fit = budget > shared ? (budget - shared) / per_set : 0;
+  if (fit == 0) {
     std::fprintf(stderr, "inputs do not fit: need %.2f GB, %.2f GB usable\n",
-                 (fixed + set_bytes) / 1e9, usable / 1e9);
+                 (shared + per_set) / 1e9, budget / 1e9);
     return kNoMemory;
   }
-  const int nsets = static_cast<int>(std::min<std::size_t>(kMaxSets, room / set_bytes));
+  const int nsets = static_cast<int>(std::min<std::size_t>(kMaxSets, fit));
+  const std::size_t flush_bytes = opt.flush ? kFlushBytes : 0;
   std::vector<std::string> notes;
   if (opt.smoke) notes.push_back("smoke");
   if (p.causal) notes.push_back("flops=causal_half");

@@ -6,7 +6,6 @@
                 Exports exactly the functions of include/fa/attention.h.
   _C.so         csrc/ext.cpp against PyTorch-ROCm, linked to libfa_hip.so (rpath $ORIGIN).
   bench/fa_bench  the torch-free benchmark binary (bench/fa_bench.hip), linked to libfa_hip.so.
-  bench/issue_probe, bench/phase_clocks  the cycle-budget measurement tools (standalone).
 
 Both land in fused-attention-cuda_amd/fused_attn/, next to the Python package that loads them.
 Object files go to fused-attention-cuda_amd/_build/. Every call rebuilds everything (the build
@@ -105,14 +104,6 @@ def build(jobs: int = 8) -> None:
     run([HIPCC, *HIP_FLAGS, str(bench_src), "-o", str(tmp), f"-L{OUT}", "-lfa_hip",
          "-Wl,-rpath,$ORIGIN/../fused_attn"])
     os.replace(tmp, bench_bin)
-
-    # Measurement tools of the cycle budget: the issue / bandwidth probes and the stage-5 kernel
-    # compiled with its phase clocks (neither links the library).
-    for tool in ("issue_probe", "phase_clocks"):
-        out = PKG_ROOT / "bench" / tool
-        tmp = out.with_suffix(".tmp")
-        run([HIPCC, *HIP_FLAGS, str(PKG_ROOT / "bench" / f"{tool}.hip"), "-o", str(tmp)])
-        os.replace(tmp, out)
 
     cflags, ldflags = torch_flags()
     ext_obj = BUILD / "ext.cpp.o"

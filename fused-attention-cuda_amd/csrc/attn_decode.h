@@ -50,6 +50,11 @@ __device__ __forceinline__ void dec_dma16(const void* src, uint32_t lds) {
 template <typename T, int D, int RG>
 struct Dec16 {
   using F = Fa16<T, D, RG, 4, 32, true>;
+  // The decode's LDS: F's double-buffered K/V tiles, reused for the key-split merge at the end.
+  // (F's own kLdsBytes also counts the Q region of the forward's prologue, which the decode, with
+  // its query rows in registers, does not have.)
+  static constexpr size_t kLdsBytes =
+      F::kTileBytes > F::kMergeBytes ? F::kTileBytes : F::kMergeBytes;
   static constexpr int BC = F::BC;        // 128 keys per tile
   static constexpr int kWaves = F::kWaves;
   static constexpr int kThreads = F::kThreads;
@@ -71,7 +76,7 @@ struct Dec16 {
   }
 
   __device__ static void run(const DecArgs& a) {
-    __shared__ __attribute__((aligned(16))) char lds_raw[F::kLdsBytes];
+    __shared__ __attribute__((aligned(16))) char lds_raw[kLdsBytes];
     T* lds = reinterpret_cast<T*>(lds_raw);
     const int tid = threadIdx.x;
     const int lane = tid & 63;

@@ -78,22 +78,6 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef s16x4 __attribute__((address_space(3))) lds_s16x4;
 
-// Phase clocks: a diagnostic build (bench/phase_clocks.hip defines FA_PHASE_CLOCKS) records, per
-// wave of stage 5, 8 words: s_memtime at the start, after the prologue barrier, after the key walk
-// and at the end; the s_memtime cycles spent in the step barriers (the wait for the slowest wave);
-// s_memrealtime (100 MHz) at the start and the end; the number of steps in the low 32 bits of the
-// last word, with the wave's XCC (hardware register XCC_ID, 4 bits) at bit 32 and the low 24 bits
-// of its HW_ID (wave, SIMD, CU, shader array and engine) at bit 40. The library itself is built
-// without it, and then none of this code exists.
-#if defined(FA_PHASE_CLOCKS)
-constexpr int kClockMaxWorkgroups = 4096;
-__device__ unsigned long long fa_phase_clocks[kClockMaxWorkgroups * 16 * 8];
-#define FA_CLK(i, v) clk[i] = (v)
-#define FA_CLK_ADD(i, v) clk[i] += (v)
-#else
-#define FA_CLK(i, v) ((void)0)
-#define FA_CLK_ADD(i, v) ((void)0)
-#endif
 constexpr float kLn2 = 0.69314718055994531f;
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -577,25 +561,6 @@ struct Fa16 {
     const int rg = wave % RG;
     const int ks = wave / RG;
     const int g = lane >> 5;
-#if defined(FA_PHASE_CLOCKS)
-    unsigned long long clk[8] = {};
-    const auto clk_store = [&] {
-      clk[3] = __builtin_amdgcn_s_memtime();
-      clk[6] = __builtin_amdgcn_s_memrealtime();
-      // s_getreg operand: register id | offset << 6 | (bits - 1) << 11; XCC_ID is 20, HW_ID 4.
-      const unsigned long long xcc = __builtin_amdgcn_s_getreg(20 | (3 << 11)) & 15u;
-      const unsigned long long hw = __builtin_amdgcn_s_getreg(4 | (31 << 11)) & 0xffffffu;
-      clk[7] = (clk[7] & 0xffffffffull) | (xcc << 32) | (hw << 40);
-      if (lane == 0 && PIPE && blockIdx.x < kClockMaxWorkgroups) {
-        unsigned long long* d = fa_phase_clocks + (static_cast<size_t>(blockIdx.x) * 16 + wave) * 8;
-        for (int i = 0; i < 8; ++i) d[i] = clk[i];
-      }
-    };
-    clk[0] = __builtin_amdgcn_s_memtime();
-    clk[5] = __builtin_amdgcn_s_memrealtime();
-#else
-    const auto clk_store = [] {};
-#endif
 
     // XCD-aware decode of the 1-D grid into (head, query tile, part). (readfirstlane: uniform
     // integer divisions run on the vector unit, and their results would otherwise occupy vector
@@ -718,7 +683,6 @@ struct Fa16 {
       }
       wait_dma();
       __syncthreads();  // V(t0), K(t0+1) visible; K buffer 0 is refilled in iteration 0
-      FA_CLK(1, __builtin_amdgcn_s_memtime());
       // One pipeline step. `full` (a compile-time tag) selects the steady-state body: tiles t and
       // t+1 are full for every wave of the workgroup and carry no causal diagonal, so the body has
       // no per-block branches and the VALU softmax of S(t) interleaves with the MFMAs of S(t+1).
@@ -759,13 +723,8 @@ struct Fa16 {
             pv<false>(ws, P, vc, vl, nv, dg);
           }
         }
-#if defined(FA_PHASE_CLOCKS)
-        const unsigned long long clk_b = __builtin_amdgcn_s_memtime();
-#endif
         wait_dma();
         __syncthreads();
-        FA_CLK_ADD(4, __builtin_amdgcn_s_memtime() - clk_b);
-        FA_CLK_ADD(7, 1);
       };
       using Full = std::true_type;
       using Part = std::false_type;
@@ -818,7 +777,6 @@ struct Fa16 {
       }
     }
 
-    FA_CLK(2, __builtin_amdgcn_s_memtime());
     // ---- merge the KS partial states of each row group (LDS is free after the last barrier) ----
     if constexpr (KS > 1) {
       float* mg = reinterpret_cast<float*>(lds_raw);
@@ -833,10 +791,7 @@ struct Fa16 {
         dst[(kDB * 16 + 1) * 64 + lane] = ws.l;
       }
       __syncthreads();
-      if (ks > 0) {
-        clk_store();
-        return;
-      }
+      if (ks > 0) return;
 #pragma unroll
       for (int sp = 1; sp < KS; ++sp) {
         const float* src = mg + ((sp - 1) * RG + rg) * kMergeFloats;
@@ -860,10 +815,7 @@ struct Fa16 {
 
     // ---- epilogue: O = acc / l, lse = m*scale + ln l (ref:include/fa/softmax_math.cuh:58-71) ----
     const float lt = halves_sum(ws.l);
-    if (!wave_valid) {
-      clk_store();
-      return;
-    }
+    if (!wave_valid) return;
     const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
     if (S > 1) {
       // One part of a split walk: its normalised O in fp32 and its LSE (-inf when the part saw
@@ -886,7 +838,6 @@ struct Fa16 {
                                ? ws.m * a.scale + log2_hw(lt) * kLn2
                                : -__builtin_inff();
       }
-      clk_store();
       return;
     }
     T* orow = static_cast<T*>(a.o) + b * a.osb + h * a.osh + row * a.osn;
@@ -911,7 +862,6 @@ struct Fa16 {
           (lt > 0.f && ws.m != -__builtin_inff()) ? ws.m * a.scale + log2_hw(lt) * kLn2
                                                    : __builtin_inff();
     }
-    clk_store();
   }
 };
 
@@ -1038,32 +988,34 @@ constexpr Variant variant() {
 // workgroup; tests/test_register_budget_cpu.py checks the compiler's report for every kernel);
 // that is what rules out BCW = 64 at D = 128 with 8 waves, BR 256 / BC 128, and BR 256 / BC 64 at
 // D = 128 (8 x 32 rows with 64 keys per wave: 53 registers spilled to scratch).
-template <typename T, int D>
+template <typename T, int D, int STAGE>
 struct S5Rows {
   static constexpr Variant rows[] = {
-      variant<5, T, D, 1, 1, 32>(),  // BR  32, BC  32
-      variant<5, T, D, 1, 2, 32>(),  // BR  32, BC  64 (2-way split)
-      variant<5, T, D, 2, 1, 32>(),  // BR  64, BC  32
-      variant<5, T, D, 2, 2, 32>(),  // BR  64, BC  64 (2-way split)
-      variant<5, T, D, 2, 2, 64>(),  // BR  64, BC 128 (2-way split, 4 waves)
-      variant<5, T, D, 4, 1, 32>(),  // BR 128, BC  32
-      variant<5, T, D, 4, 2, 32>(),  // BR 128, BC  64 (2-way split) -- D = 128 default
+      variant<STAGE, T, D, 1, 1, 32>(),  // BR  32, BC  32
+      variant<STAGE, T, D, 1, 2, 32>(),  // BR  32, BC  64 (2-way split)
+      variant<STAGE, T, D, 2, 1, 32>(),  // BR  64, BC  32
+      variant<STAGE, T, D, 2, 2, 32>(),  // BR  64, BC  64 (2-way split)
+      variant<STAGE, T, D, 2, 2, 64>(),  // BR  64, BC 128 (2-way split, 4 waves)
+      variant<STAGE, T, D, 4, 1, 32>(),  // BR 128, BC  32
+      variant<STAGE, T, D, 4, 2, 32>(),  // BR 128, BC  64 (2-way split) -- D = 128 default
   };
 };
 
 // At D = 64 only: BR 128 / BC 128 (4 row groups x 2 key splits of 64 keys, the D = 64 default),
 // BR 32 / BC 128 (the same waves, one row group), the height small grids are launched with, and
 // BR 256 / BC 64.
-template <typename T>
+// STAGE 5 is the table stage 5 launches; STAGE 4 gives the same tiles with the synchronous loop
+// (launched as fa_s4_mfma), which stage 5 runs under FA_S5_PREFETCH=0.
+template <typename T, int STAGE = 5>
 VariantList s5_table() {
+  using R64 = S5Rows<T, 64, STAGE>;
+  using R128 = S5Rows<T, 128, STAGE>;
   static const Variant t[] = {
-      S5Rows<T, 64>::rows[0],  S5Rows<T, 64>::rows[1],  S5Rows<T, 64>::rows[2],
-      S5Rows<T, 64>::rows[3],  S5Rows<T, 64>::rows[4],  S5Rows<T, 64>::rows[5],
-      S5Rows<T, 64>::rows[6],  variant<5, T, 64, 8, 1, 64>(),  variant<5, T, 64, 4, 2, 64>(),
-      variant<5, T, 64, 1, 2, 64>(),
-      S5Rows<T, 128>::rows[0], S5Rows<T, 128>::rows[1], S5Rows<T, 128>::rows[2],
-      S5Rows<T, 128>::rows[3], S5Rows<T, 128>::rows[4], S5Rows<T, 128>::rows[5],
-      S5Rows<T, 128>::rows[6]};
+      R64::rows[0],  R64::rows[1],  R64::rows[2],  R64::rows[3],
+      R64::rows[4],  R64::rows[5],  R64::rows[6],  variant<STAGE, T, 64, 8, 1, 64>(),
+      variant<STAGE, T, 64, 4, 2, 64>(),  variant<STAGE, T, 64, 1, 2, 64>(),
+      R128::rows[0], R128::rows[1], R128::rows[2], R128::rows[3],
+      R128::rows[4], R128::rows[5], R128::rows[6]};
   return VariantList{t, static_cast<int>(sizeof(t) / sizeof(t[0]))};
 }
 

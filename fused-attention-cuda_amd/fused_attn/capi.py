@@ -34,7 +34,7 @@ EXPORTS = ("fa_forward", "fa_forward_strided", "fa_workspace_bytes", "fa_impl_su
            "fa_decode_workspace_bytes", "fa_decode", "fa_decode_noalloc")
 
 # FA_DECODE_SCRATCH_BYTES of include/fa/attention.h: the scratch behind fa_decode_noalloc.
-DECODE_SCRATCH_BYTES = 16 << 20
+DECODE_SCRATCH_BYTES = 17 << 20
 
 
 class FaParams(ctypes.Structure):

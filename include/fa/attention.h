@@ -172,8 +172,11 @@ FA_API int fa_decode(int dtype, const void* q, const void* k, const void* v, voi
                      void* workspace, const fa_decode_params* p, hipStream_t stream);
 
 /* Bytes of device scratch behind fa_decode_noalloc: one fixed array per GPU, held from the moment
- * the library's code is loaded on that GPU until the process ends. */
-#define FA_DECODE_SCRATCH_BYTES (16u << 20)
+ * the library's code is loaded on that GPU until the process ends. Sized for every problem the
+ * automatic split count allows (num_splits = 0): that count keeps B*Hkv*S at most B*Hkv + 255
+ * split groups, and 510 groups of 64 rows of D = 128 fp32 partials (plus their LSE) take
+ * 16,842,240 bytes. */
+#define FA_DECODE_SCRATCH_BYTES (17u << 20)
 
 /* fa_decode with no workspace argument and no allocation of any kind: the splits' partial O and
  * LSE go to the library's device-resident scratch array (FA_DECODE_SCRATCH_BYTES per GPU) instead
@@ -184,7 +187,9 @@ FA_API int fa_decode(int dtype, const void* q, const void* k, const void* v, voi
  * FA_DECODE_SCRATCH_BYTES (ask for fewer splits, or use fa_decode with a workspace). Every call on
  * one GPU shares that GPU's array: calls that may overlap on one GPU (different streams, or
  * different host threads) race and must be serialised by the caller. The first call on each GPU
- * looks up the array's device address (hipGetSymbolAddress, no allocation). */
+ * looks up the array's device address (hipGetSymbolAddress, no allocation): make that first call
+ * outside a stream capture (a warm-up call, or any call before capturing); later calls are plain
+ * kernel launches and may be captured. */
 FA_API int fa_decode_noalloc(int dtype, const void* q, const void* k, const void* v, void* o,
                              float* lse, const fa_decode_params* p, hipStream_t stream);
 

@@ -27,9 +27,9 @@ def table_variants() -> list[tuple[int, int, int, int]]:
     """(D, RG, KS, BCW) of every stage-5 and stage-4 variant instantiated in attn_mfma16.h."""
     src = (CSRC / "attn_mfma16.h").read_text()
     rows = src[src.index("struct S5Rows"):src.index("};", src.index("struct S5Rows"))]
-    generic = re.findall(r"variant<5, T, D, (\d+), (\d+), (\d+)>", rows)
+    generic = re.findall(r"variant<STAGE, T, D, (\d+), (\d+), (\d+)>", rows)
     found = {(d, *map(int, g)) for d in (64, 128) for g in generic}
-    for m in re.finditer(r"variant<[45], T, (\d+), (\d+), (\d+), (\d+)>", src):
+    for m in re.finditer(r"variant<(?:[45]|STAGE), T, (\d+), (\d+), (\d+), (\d+)>", src):
         found.add(tuple(map(int, m.groups())))
     return sorted(found)
 

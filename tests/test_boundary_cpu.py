@@ -229,3 +229,24 @@ def test_product_sources_never_reach_the_oracle():
         if path.suffix in {".h", ".cpp", ".hip", ".py"}:
             text = path.read_text()
             assert "oracle" not in text.lower().replace("oracle-free", ""), path
+
+
+def test_noalloc_scratch_holds_every_automatic_split():
+    """fa_decode_noalloc serves every problem whose split count the library picks itself
+    (num_splits = 0): for B*Hkv from 1 to 300 split groups, up to 64 query rows per kv head and
+    D = 64 or 128 on a long cache, the partials of the automatic split count fit the scratch
+    array. B*Hkv = 255 with 64 rows of D = 128 is the largest (2 splits, 16,842,240 bytes)."""
+    lib = capi.load()
+    text = HEADER.read_text()
+    m = re.search(r"#define FA_DECODE_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
+    assert m is not None
+    assert int(m.group(1)) << int(m.group(2)) == capi.DECODE_SCRATCH_BYTES
+    worst = 0
+    for groups in range(1, 301):
+        for g, nq in ((1, 1), (4, 4), (16, 4), (64, 1)):
+            for d in (64, 128):
+                p = capi.FaDecodeParams(groups, g, 1, nq, 1 << 20, d, 0.125, True, 0)
+                need = lib.fa_decode_workspace_bytes(capi.FA_DTYPE_BF16, ctypes.byref(p))
+                assert need <= capi.DECODE_SCRATCH_BYTES, (groups, g, nq, d, need)
+                worst = max(worst, need)
+    assert worst == 16_842_240

@@ -82,3 +82,33 @@ def test_noalloc_without_split_needs_no_scratch():
     assert capi.decode_noalloc(q, k, v, o, lse, False, 0.125) == capi.HIP_SUCCESS
     torch.cuda.synchronize()
     assert torch.equal(o, o_ref) and torch.equal(lse, lse_ref)
+
+
+def test_noalloc_replays_from_a_captured_graph():
+    """The entry point's purpose: a caller that captures the decode into a HIP graph. The first
+    call on the device runs outside the capture (it resolves the scratch array's address); the
+    captured call is then replayed twice, with the outputs cleared by eager work in between, and
+    each replay must equal fa_decode bit for bit."""
+    b, h, hkv, nq, nkv, d = 2, 16, 4, 2, 4096 + 40, 128
+    q, k, v = _inputs(b, h, hkv, nq, nkv, d, torch.bfloat16, seed=52)
+    scale = d ** -0.5
+    assert capi.load().fa_decode_num_splits(capi.decode_params(q, k, True, scale)) > 1
+    o_ref, lse_ref = _outputs(q)
+    assert capi.decode(q, k, v, o_ref, lse_ref, True, scale) == capi.HIP_SUCCESS
+    o, lse = _outputs(q)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        assert capi.decode_noalloc(q, k, v, o, lse, True, scale, stream=stream) == capi.HIP_SUCCESS
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        rc = capi.decode_noalloc(q, k, v, o, lse, True, scale, stream=stream)
+    assert rc == capi.HIP_SUCCESS, capi.error_string(rc)
+    for replay in range(2):
+        o.fill_(float("nan"))
+        lse.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()
+        stream.synchronize()
+        assert torch.equal(o, o_ref) and torch.equal(lse, lse_ref), f"replay {replay}"
