@@ -591,8 +591,17 @@ struct Fa16 {
     // Key range of the workgroup (causal stops at its last row) and of this wave. The workgroup
     // walks key tiles [t0, n_tiles): the whole walk, or its part of a split walk; steps before
     // n_steady take the steady body (layout::plan_walk).
-    const layout::Walk walk = layout::plan_walk(N, BC, kBr, qt, a.causal != 0, part,
-                                                [&](int x) { return fdiv(x, a.fd_splits); });
+    layout::Walk walk = layout::plan_walk(N, BC, kBr, qt, a.causal != 0, part,
+                                          [&](int x) { return fdiv(x, a.fd_splits); });
+    if (PIPE && a.rotate) {
+      layout::rotate_walk(walk, N, BC, kBr, qt, a.causal != 0, part,
+                          [&](int x) { return fdiv(x, a.fd_splits); },
+                          [&](int x) { return fdiv(x, a.fd_rot_blocks); });
+    }
+    walk.rot = __builtin_amdgcn_readfirstlane(walk.rot);
+    walk.rot_end = __builtin_amdgcn_readfirstlane(walk.rot_end);
+    // Key tile of walk step t (in order, or rotated: layout::walk_tile).
+    auto wt = [&](int t) { return layout::walk_tile(walk, t); };
     const int t0 = __builtin_amdgcn_readfirstlane(walk.t0);
     const int n_tiles = __builtin_amdgcn_readfirstlane(walk.n_tiles);
     const int wave_end = wave_valid ? (a.causal ? min(N, r0 + 32) : N) : 0;
@@ -653,10 +662,10 @@ struct Fa16 {
           const int qrow = min(i0 + src.row, N - 1);
           dma_asm(qtile + src.off + (qrow - src.row) * a.qsn, qbuf + 512 * (wave + i * kWaves));
         }
-        dma_tile_asm<false>(kbuf0, kg, dk, t0 * BC, N, ksn, wave);
-        dma_tile_asm<true>(vbuf0, vg, dv, t0 * BC, N, vsn, wave);
+        dma_tile_asm<false>(kbuf0, kg, dk, wt(t0) * BC, N, ksn, wave);
+        dma_tile_asm<true>(vbuf0, vg, dv, wt(t0) * BC, N, vsn, wave);
         if (t0 + 1 < n_tiles) {
-          dma_tile_asm<false>(kbuf0 + kKElems, kg, dk, (t0 + 1) * BC, N, ksn, wave);
+          dma_tile_asm<false>(kbuf0 + kKElems, kg, dk, wt(t0 + 1) * BC, N, ksn, wave);
           wait_dma_but<2 * kDmaPerWave>();
         } else {
           wait_dma_but<kDmaPerWave>();
@@ -668,7 +677,7 @@ struct Fa16 {
       }
       f32x16 sa[kKB], sb[kKB];
       {
-        const int nv0 = nvalid_of(t0);
+        const int nv0 = nvalid_of(wt(t0));
         if (nv0 > 0) qk<false>(sa, ws, kwave(0), nv0, kl);
       }
       // When the first step is a steady one (tile t0 full and free of the causal diagonal), the
@@ -702,7 +711,7 @@ struct Fa16 {
           // two steps when every tile is full) the copies land in buffers that are not read again
           // (the last step's S(t+1) is computed from a stale K buffer and discarded), which keeps
           // the tail on this branch-free body.
-          const int tk = min(t + 2, n_tiles - 1), tv = min(t + 1, n_tiles - 1);
+          const int tk = wt(min(t + 2, n_tiles - 1)), tv = wt(min(t + 1, n_tiles - 1));
           step_full(ws, s_cur, s_nxt, P, kn, vc, kl, vl, c, lane, [&] {
             dma_tile_full<false>(kbuf0 + (u & 1) * kKElems, kg, dk, tk * BC, ksn, wave);
             dma_tile_full<true>(vbuf0 + ((u + 1) & 1) * kVElems, vg, dv, tv * BC, vsn, wave);

@@ -73,11 +73,24 @@ FA_HD constexpr int v_operand_offset(int lane, int db) {
 // tile of the walk) are whole tiles inside the tensor. The rule, in the kernel's words: when every
 // tile of the walk is full, all of them take the steady step; otherwise step t needs tile t full
 // and free of the causal diagonal, t + 1 inside the walk, and t + 3 <= N / BC.
+//
+// Walk order. Tiles are walked in the order walk_tile(w, t0), walk_tile(w, t0 + 1), ...: the
+// range [t0, rot_end) rotated left by `rot` (0 <= rot < rot_end - t0; rot_end <= n_steady), then
+// the rest in order. Workgroups that share a head's K/V start their rotations at different tiles,
+// so that a tile one of them fetches from HBM is found in L2 by the others a few steps later
+// instead of all of them waiting on the same miss at once (rotate_walk).
 struct Walk {
   int t0;
   int n_tiles;
   int n_steady;
+  int rot;
+  int rot_end;
 };
+FA_HD inline int walk_tile(const Walk& w, int t) {
+  if (t >= w.rot_end) return t;
+  const int x = t + w.rot;
+  return x < w.rot_end ? x : x - (w.rot_end - w.t0);
+}
 // div_splits(x) must return x / splits (the kernel passes its multiply-shift division).
 template <typename DivSplits>
 FA_HD inline Walk plan_walk(int N, int BC, int BR, int qt, bool causal, int part,
@@ -86,6 +99,8 @@ FA_HD inline Walk plan_walk(int N, int BC, int BR, int qt, bool causal, int part
   const int kv_end = causal ? (N < i0 + BR ? N : i0 + BR) : N;
   const int n_walk = (kv_end + BC - 1) / BC;
   Walk w;
+  w.rot = 0;
+  w.rot_end = 0;
   w.t0 = div_splits(part * n_walk);
   w.n_tiles = div_splits((part + 1) * n_walk);
   const int n_full = (causal ? i0 : N) / BC;
@@ -97,6 +112,24 @@ FA_HD inline Walk plan_walk(int N, int BC, int BR, int qt, bool causal, int part
     w.n_steady = s > w.t0 ? s : w.t0;
   }
   return w;
+}
+
+// The rotation of a workgroup's walk. It is a property of the 128-row block (kRotRows) that holds
+// the workgroup's first row, so that every workgroup height (32, 64 or 128 rows) gives each 32-row
+// wave the same sequence of key tiles, hence the same results: the rotated range is the block's
+// steady range [t0, n_steady of a 128-row workgroup at the block), which lies inside the steady
+// range of any shorter workgroup of the block, and block blk of n_blocks starts blk / n_blocks of
+// the way round it. div_blocks(x) must return x / n_blocks, n_blocks = ceil(N / kRotRows).
+constexpr int kRotRows = 128;
+template <typename DivSplits, typename DivBlocks>
+FA_HD inline void rotate_walk(Walk& w, int N, int BC, int BR, int qt, bool causal, int part,
+                              DivSplits div_splits, DivBlocks div_blocks) {
+  const int blk = qt * BR / kRotRows;
+  const Walk wb = plan_walk(N, BC, kRotRows, blk, causal, part, div_splits);
+  const int end = wb.n_steady < w.n_steady ? wb.n_steady : w.n_steady;
+  if (wb.t0 != w.t0 || end - w.t0 < 2) return;
+  w.rot_end = end;
+  w.rot = div_blocks(blk * (end - w.t0));
 }
 
 // The work item of workgroup `bid` of a stage-4/5 grid of G = n_qtiles * BH * splits workgroups

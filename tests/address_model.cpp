@@ -159,13 +159,30 @@ void check_q_load(const Variant& v, int N, int sn, int qt, const std::string& c)
 // The load schedule of one stage-5 (pipelined) or stage-4 (synchronous) workgroup.
 template <int D>
 void replay_workgroup(const Variant& v, int N, int sn, bool causal, int S, int part, int qt,
-                      bool pipelined) {
+                      bool pipelined, bool rotate) {
   const int BC = v.KS * v.BCW, BR = 32 * v.RG;
-  const auto walk = fa::layout::plan_walk(N, BC, BR, qt, causal, part,
-                                          [S](int x) { return x / S; });
+  auto walk = fa::layout::plan_walk(N, BC, BR, qt, causal, part, [S](int x) { return x / S; });
+  const int n_blocks = (N + fa::layout::kRotRows - 1) / fa::layout::kRotRows;
+  if (rotate && pipelined) {
+    fa::layout::rotate_walk(walk, N, BC, BR, qt, causal, part, [S](int x) { return x / S; },
+                            [n_blocks](int x) { return x / n_blocks; });
+  }
+  auto wt = [&](int t) { return fa::layout::walk_tile(walk, t); };
   const std::string c = ctx(v, N, sn, causal, S, part, qt);
-  if (walk.t0 > walk.n_tiles || walk.n_steady < walk.t0 || walk.n_steady > walk.n_tiles) {
+  if (walk.t0 > walk.n_tiles || walk.n_steady < walk.t0 || walk.n_steady > walk.n_tiles ||
+      walk.rot < 0 || walk.rot_end > walk.n_steady ||
+      (walk.rot > 0 && walk.rot >= walk.rot_end - walk.t0)) {
     fail("inconsistent walk plan: " + c);
+  }
+  // The rotated order visits every tile of the walk exactly once.
+  {
+    std::vector<int> seen(walk.n_tiles, 0);
+    for (int t = walk.t0; t < walk.n_tiles; ++t) {
+      const int k = wt(t);
+      if (k < walk.t0 || k >= walk.n_tiles || seen[k]++) fail("walk order is not a permutation: " + c);
+      if ((t < walk.n_steady) != (k < walk.n_steady)) fail("rotation leaves the steady range: " + c);
+      ++g_checks;
+    }
   }
   if (walk.t0 == walk.n_tiles) return;  // an empty part of a split walk loads nothing
   if (!pipelined) {
@@ -177,14 +194,14 @@ void replay_workgroup(const Variant& v, int N, int sn, bool causal, int S, int p
   }
   // Prologue: Q, K(t0), V(t0), K(t0 + 1).
   check_q_load<D>(v, N, sn, qt, c + " (Q)");
-  check_tile_load<D, false>(v, N, sn, walk.t0 * BC, true, c);
-  check_tile_load<D, true>(v, N, sn, walk.t0 * BC, true, c);
-  if (walk.t0 + 1 < walk.n_tiles) check_tile_load<D, false>(v, N, sn, (walk.t0 + 1) * BC, true, c);
+  check_tile_load<D, false>(v, N, sn, wt(walk.t0) * BC, true, c);
+  check_tile_load<D, true>(v, N, sn, wt(walk.t0) * BC, true, c);
+  if (walk.t0 + 1 < walk.n_tiles) check_tile_load<D, false>(v, N, sn, wt(walk.t0 + 1) * BC, true, c);
   for (int t = walk.t0; t < walk.n_tiles; ++t) {
     if (t < walk.n_steady) {
       // Steady step: K(t + 2) and V(t + 1) clamped to the walk's last tile, loaded unclamped.
-      const int tk = t + 2 < walk.n_tiles - 1 ? t + 2 : walk.n_tiles - 1;
-      const int tv = t + 1 < walk.n_tiles - 1 ? t + 1 : walk.n_tiles - 1;
+      const int tk = wt(t + 2 < walk.n_tiles - 1 ? t + 2 : walk.n_tiles - 1);
+      const int tv = wt(t + 1 < walk.n_tiles - 1 ? t + 1 : walk.n_tiles - 1);
       check_tile_load<D, false>(v, N, sn, tk * BC, false, c + " (steady K)");
       check_tile_load<D, true>(v, N, sn, tv * BC, false, c + " (steady V)");
     } else {
@@ -219,8 +236,10 @@ void sweep_variant(const Variant& v) {
         for (int S : {1, 2, 3, 5, 16}) {
           for (int part = 0; part < S; ++part) {
             for (int qt = 0; qt < n_qtiles; ++qt) {
-              replay_workgroup<D>(v, N, sn, causal, S, part, qt, true);
-              if (S == 1) replay_workgroup<D>(v, N, sn, causal, 1, 0, qt, false);
+              for (const bool rotate : {false, true}) {
+                replay_workgroup<D>(v, N, sn, causal, S, part, qt, true, rotate);
+              }
+              if (S == 1) replay_workgroup<D>(v, N, sn, causal, 1, 0, qt, false, false);
               if (S > 1) check_split_rows(N, D, S, part, qt * BR,
                                           qt * BR + BR < N ? qt * BR + BR : N);
             }
@@ -322,6 +341,41 @@ void check_grid_items() {
 
 }  // namespace
 
+// The rotated walk order keeps results independent of the workgroup height: every 32-row wave
+// meets the same key tiles in the same order at heights 32, 64 and 128 (the kernel computes a
+// wave's rows from its own tiles only, so equal tile sequences give equal bits). A wave's sequence
+// is the walk order of its workgroup restricted to the tiles holding a key it can see.
+void check_rotation_height_invariance() {
+  for (int BC : {32, 64, 128}) {
+    for (int N : {32, 96, 128, 224, 512, 640, 1024, 1056, 2048}) {
+      for (bool causal : {false, true}) {
+        const int n_blocks = (N + fa::layout::kRotRows - 1) / fa::layout::kRotRows;
+        for (int r0 = 0; r0 < N; r0 += 32) {
+          std::vector<std::vector<int>> seqs;
+          for (int BR : {128, 64, 32}) {
+            const int qt = r0 / BR;
+            auto w = fa::layout::plan_walk(N, BC, BR, qt, causal, 0, [](int x) { return x; });
+            fa::layout::rotate_walk(w, N, BC, BR, qt, causal, 0, [](int x) { return x; },
+                                    [n_blocks](int x) { return x / n_blocks; });
+            const int wave_end = causal ? (r0 + 32 < N ? r0 + 32 : N) : N;
+            std::vector<int> seq;
+            for (int t = w.t0; t < w.n_tiles; ++t) {
+              const int k = fa::layout::walk_tile(w, t);
+              if (k * BC < wave_end) seq.push_back(k);
+            }
+            seqs.push_back(seq);
+            ++g_checks;
+          }
+          if (seqs[0] != seqs[1] || seqs[0] != seqs[2]) {
+            fail("rotated walk differs between heights: BC=" + std::to_string(BC) + " N=" +
+                 std::to_string(N) + (causal ? " causal" : "") + " rows " + std::to_string(r0));
+          }
+        }
+      }
+    }
+  }
+}
+
 int main(int argc, char** argv) {
   // Arguments: D,RG,KS,BCW for each stage-4/5 variant of the kernel tables.
   int n = 0;
@@ -340,6 +394,7 @@ int main(int argc, char** argv) {
   sweep_decode<64>();
   sweep_decode<128>();
   check_grid_items();
+  check_rotation_height_invariance();
   std::printf("address model: %d variants, decode and the grid decode, %lld checks, all in bounds\n",
               n, g_checks);
   return 0;

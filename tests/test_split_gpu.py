@@ -26,6 +26,7 @@ import torch
 import fused_attn
 from _checks import check_against_reference
 from fused_attn import capi
+from oracle.oracle import math_reference
 
 pytestmark = pytest.mark.gpu
 
@@ -178,3 +179,29 @@ def test_gqa_splits(hkv, dtype, monkeypatch):
     for causal in (False, True):
         o, lse = _split_run(q, k, v, causal, 1.0 / math.sqrt(128))
         check_against_reference(o, q, k, v, causal, dtype, lse=lse)
+
+
+@pytest.mark.parametrize("b,h,n,d,dtype,causal", [
+    (2, 8, 1024, 128, torch.float16, False),
+    (2, 4, 768, 64, torch.float16, True),
+    (1, 8, 1056, 128, torch.bfloat16, True),
+    (2, 2, 640, 64, torch.bfloat16, False),
+], ids=lambda x: str(x))
+def test_rotated_and_in_order_walks_both_meet_the_oracle(b, h, n, d, dtype, causal, monkeypatch):
+    """The key walk's order (in order, or rotated per 128-row block so that workgroups sharing a
+    head fetch different tiles at a time) only reorders each row's accumulation: both orders meet
+    the fp64 oracle, forced either way with the test-only FA_FORCE_ROTATE."""
+    gen = torch.Generator().manual_seed(31)
+    q, k, v = (torch.randn(b, h, n, d, generator=gen).to("cuda", dtype) for _ in range(3))
+    ref, lse64 = math_reference(q, k, v, is_causal=causal)
+    outs = []
+    for force in ("0", "1"):
+        monkeypatch.setenv("FA_FORCE_ROTATE", force)
+        o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
+        torch.cuda.synchronize()
+        err = float(abs(o.double().cpu().numpy() - ref).max())
+        lerr = float(abs(lse.double().cpu().numpy() - lse64).max())
+        tol = 2e-3 + (2e-3 if dtype == torch.float16 else 2 ** -8) * float(abs(ref).max())
+        assert err <= tol, f"FA_FORCE_ROTATE={force}: O error {err:.3e}"
+        assert lerr <= 1e-3, f"FA_FORCE_ROTATE={force}: LSE error {lerr:.3e}"
+    monkeypatch.delenv("FA_FORCE_ROTATE")
