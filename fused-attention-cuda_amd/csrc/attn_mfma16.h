@@ -567,10 +567,11 @@ struct Fa16 {
     // registers for the whole kernel.)
     const layout::Item item = layout::grid_item(
         static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), a.n_qtiles, a.n_splits,
-        a.causal != 0, a.xcd_heads,
+        a.causal != 0, a.xcd_heads, a.xcd_cus,
         [&](int x) { return __builtin_amdgcn_readfirstlane(fdiv(x, a.fd_splits)); },
         [&](int x) { return __builtin_amdgcn_readfirstlane(fdiv(x, a.fd_qtiles)); },
-        [&](int x) { return __builtin_amdgcn_readfirstlane(fdiv(x, a.fd_xcd_heads)); });
+        [&](int x) { return __builtin_amdgcn_readfirstlane(fdiv(x, a.fd_xcd_heads)); },
+        [&](int x) { return __builtin_amdgcn_readfirstlane(fdiv(x, a.fd_xcd_cus)); });
     const int S = a.n_splits;
     const int part = __builtin_amdgcn_readfirstlane(item.part);
     const int bh = __builtin_amdgcn_readfirstlane(item.bh);
@@ -961,6 +962,25 @@ int launch_combine(const KArgs& a, hipStream_t stream) {
   return static_cast<int>(hipGetLastError());
 }
 
+// Workgroups of one variant resident per CU at once (the runtime's occupancy for its registers and
+// LDS), asked once per process; 1 if the query fails.
+template <int STAGE, typename T, int D, int RG, int KS, int BCW>
+int resident_per_cu() {
+  static const int n = [] {
+    int blocks = 0;
+    hipError_t e;
+    if constexpr (STAGE == 5) {
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fa_s5_tuned<T, D, RG, KS, BCW>,
+                                                       64 * RG * KS, 0);
+    } else {
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fa_s4_mfma<T, D, RG, KS, BCW>,
+                                                       64 * RG * KS, 0);
+    }
+    return (e == hipSuccess && blocks > 0) ? blocks : 1;
+  }();
+  return n;
+}
+
 // Host-side launch of one instantiated variant (STAGE 5 or 4).
 template <int STAGE, typename T, int D, int RG, int KS, int BCW>
 int launch(const KArgs& in, hipStream_t stream) {
@@ -970,11 +990,20 @@ int launch(const KArgs& in, hipStream_t stream) {
   a.fd_qtiles = make_fastdiv(static_cast<uint32_t>(a.n_qtiles));
   a.xcd_heads = layout::xcd_heads_for(a.B * a.H, a.causal != 0);
   a.fd_xcd_heads = make_fastdiv(static_cast<uint32_t>(a.xcd_heads > 0 ? a.xcd_heads : 1));
+  const long long grid = static_cast<long long>(a.n_qtiles) * a.B * a.H * a.n_splits;
+  // The snake order pays only when the whole grid is resident at once (every CU's workgroups are
+  // the ones the dispatcher handed out in its first rounds); once workgroups wait for free slots,
+  // the dispatcher itself balances the plain longest-first order better.
+  if (a.xcd_heads == 0 || a.n_splits != 1 ||
+      grid > static_cast<long long>(resident_per_cu<STAGE, T, D, RG, KS, BCW>()) * a.xcd_cus *
+                 layout::kXcds) {
+    a.xcd_cus = 0;
+  }
+  a.fd_xcd_cus = make_fastdiv(static_cast<uint32_t>(a.xcd_cus > 0 ? a.xcd_cus : 1));
   if (a.n_splits < 1 || (a.n_splits > 1 && (STAGE != 5 || a.o_part == nullptr ||
                                             a.lse_part == nullptr))) {
     return static_cast<int>(hipErrorInvalidValue);
   }
-  const long long grid = static_cast<long long>(a.n_qtiles) * a.B * a.H * a.n_splits;
   if (grid <= 0 || grid > 0x7fffffffLL) return static_cast<int>(hipErrorInvalidValue);
   const dim3 gr(static_cast<unsigned>(grid)), bl(A::kThreads);
   if constexpr (STAGE == 5) {

@@ -151,14 +151,29 @@ struct Item {
   int qt;
   int part;
 };
-template <typename DivS, typename DivQ, typename DivX>
+//
+// Snake order (xcd_cus > 0, tile-major and unsplit only): the dispatcher fills an XCD's CUs one
+// workgroup each, in order, before it gives any CU a second one, so with several resident
+// workgroups per CU the i-th workgroup of every round of xcd_cus shares a CU. Every second round
+// is issued in reverse, so that the longest query tile of the first round shares its CU with the
+// shortest of the second (32 + 1, 31 + 2, ... key tiles instead of 32 + 16, 31 + 15, ...).
+// div_cus(x) must return x / xcd_cus.
+template <typename DivS, typename DivQ, typename DivX, typename DivC>
 FA_HD inline Item grid_item(int bid, int G, int n_qtiles, int splits, bool causal, int xcd_heads,
-                            DivS div_splits, DivQ div_qtiles, DivX div_xcd_heads) {
+                            int xcd_cus, DivS div_splits, DivQ div_qtiles, DivX div_xcd_heads,
+                            DivC div_cus) {
   const int xcd = bid % kXcds;
-  const int local = bid / kXcds;
+  int local = bid / kXcds;
   Item it;
   int q;
   if (xcd_heads > 0) {
+    if (xcd_cus > 0 && splits == 1) {
+      const int round = div_cus(local);
+      const int first = round * xcd_cus;
+      const int per_xcd = G / kXcds;
+      const int len = per_xcd - first < xcd_cus ? per_xcd - first : xcd_cus;
+      if (round & 1) local = first + (len - 1 - (local - first));
+    }
     const int item = div_splits(local);
     it.part = local - item * splits;
     q = div_xcd_heads(item);

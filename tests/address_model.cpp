@@ -291,17 +291,22 @@ void check_grid_items() {
     for (int nq : {1, 2, 7, 16}) {
       for (int S : {1, 2, 3}) {
         for (bool causal : {false, true}) {
-          for (int order = 0; order < 2; ++order) {
+          // order 0 head-major, 1 tile-major, 2 and 3 tile-major in snake order (3 and 32 CUs
+          // per XCD).
+          for (int order = 0; order < 4; ++order) {
             const int xh = order ? fa::layout::xcd_heads_for(BH, causal) : 0;
-            if (order == 1 && xh == 0) continue;
+            if (order >= 1 && xh == 0) continue;
+            const int cus = order == 2 ? 3 : order == 3 ? 32 : 0;
             const int G = nq * BH * S;
             const std::string c = "grid BH=" + std::to_string(BH) + " nq=" + std::to_string(nq) +
                                   " S=" + std::to_string(S) + (causal ? " causal" : "") +
-                                  (order ? " tile-major" : " head-major");
+                                  (order == 0 ? " head-major" : " tile-major") +
+                                  (cus ? " snake " + std::to_string(cus) : "");
             auto decode = [&](int bid) {
               return fa::layout::grid_item(
-                  bid, G, nq, S, causal, xh, [S](int v) { return v / S; },
-                  [nq](int v) { return v / nq; }, [xh](int v) { return xh > 0 ? v / xh : 0; });
+                  bid, G, nq, S, causal, xh, cus, [S](int v) { return v / S; },
+                  [nq](int v) { return v / nq; }, [xh](int v) { return xh > 0 ? v / xh : 0; },
+                  [cus](int v) { return cus > 0 ? v / cus : 0; });
             };
             std::vector<char> seen(static_cast<size_t>(G), 0);
             std::vector<std::vector<int>> issued(fa::layout::kXcds);  // qt per XCD, issue order
@@ -314,7 +319,7 @@ void check_grid_items() {
               char& s = seen[static_cast<size_t>((it.bh * nq + it.qt) * S + it.part)];
               if (s) fail("grid item issued twice: " + c);
               s = 1;
-              if (order == 1 && it.part + 1 < S) {
+              if (order >= 1 && it.part + 1 < S) {
                 const auto nx = decode(bid + fa::layout::kXcds);
                 if (nx.bh != it.bh || nx.qt != it.qt || nx.part != it.part + 1) {
                   fail("parts of a query tile not consecutive on one XCD: " + c);
@@ -329,6 +334,19 @@ void check_grid_items() {
               for (size_t i = 1; i < q.size(); ++i) longest_first &= q[i] <= q[i - 1];
             }
             if (order == 1 && !longest_first) fail("tile-major order not longest first: " + c);
+            // Snake order: the i-th workgroups of rounds 2r and 2r + 1 share a CU; in full
+            // rounds their walks are (longest, shortest) of the pair of rounds.
+            if (order >= 2 && S == 1) {
+              for (const auto& q : issued) {
+                for (size_t r = 0; (r + 2) * cus <= q.size(); r += 2) {
+                  for (int i = 0; i + 1 < cus; ++i) {
+                    const int a0 = q[r * cus + i], a1 = q[r * cus + i + 1];
+                    const int b0 = q[(r + 1) * cus + i], b1 = q[(r + 1) * cus + i + 1];
+                    if (a1 > a0 || b1 < b0) fail("snake order rounds not opposed: " + c);
+                  }
+                }
+              }
+            }
             if (order == 0 && fa::layout::xcd_heads_for(BH, true) > 1 && nq > 1 && longest_first) {
               fail("head-major order unexpectedly longest first: " + c);
             }
