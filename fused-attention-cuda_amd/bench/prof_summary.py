@@ -7,7 +7,7 @@ Side by side:    prof_summary.py --compare LABEL=<outdir> LABEL=<outdir> ... [--
 For the attention kernels of the run (``fa_s*`` and ``fa_decode*``), per capture:
 
 * duration: the mean kernel duration from the kernel trace (the last ``last`` dispatches when
-  the program was bench.py's timed replay), TFLOP/s and share of the 2.5 PFLOP/s dense fp16/bf16
+  the program was bench.py's timed launches), TFLOP/s and share of the 2.5 PFLOP/s dense fp16/bf16
   MFMA peak (157.3 TFLOP/s for fp32); split walks add the combine kernel's mean;
 * launch: workgroups, waves per workgroup, VGPRs (architectural + accumulation), LDS bytes,
   scratch, and the occupancy they allow (waves per SIMD: 512 VGPRs per lane, 160 KiB of LDS per
@@ -137,7 +137,7 @@ def collect(outdir: str) -> dict:
     if meta.get("forced"):
         q.append(("forced", meta["forced"].strip(), "environment"))
     q.append(("kernel mean duration", f"{avg_main / 1e3:.2f} us over {len(main_d)} dispatches",
-              "kernel trace" + (f", last {last} dispatches (the timed replay)" if last else "")))
+              "kernel trace" + (f", last {last} dispatches (the last timed loop)" if last else "")))
     for k, v in others.items():
         short = re.sub(r"^_ZN\d+\w+?(fa_\w+?)I.*", r"\1", k)
         q.append((f"+ {short}", f"{v / 1e3:.2f} us", "kernel trace"))
@@ -220,7 +220,8 @@ def render(items: list[tuple[str, dict]], title: str, argv: list[str]) -> str:
                "summarised by")
     out += ["", "    python3 fused-attention-cuda_amd/bench/prof_summary.py " + " ".join(argv), ""]
     for label, c in items:
-        out.append(f"- {label + ': ' if label else ''}{c['title']}: `{c['invocation']}`")
+        inv = re.sub(r"/\S*?/repo/", "", c["invocation"])
+        out.append(f"- {label + ': ' if label else ''}{c['title']}: `{inv}`")
     out.append("")
     out.append("The rocprofv3 passes of " + (items[0][0] if items[0][0] else "the capture") +
                " (each its own run; the other captures differ only in their program arguments, "

@@ -10,8 +10,8 @@
 # The program profiled is the torch-free fa_bench, launches back to back over 4 rotating input
 # sets (FA_BENCH_FLUSH=1: a 1 GiB flush before every launch, the reference's protocol, whose
 # write-back overlaps the next launch), or, when a bench-workload is named, bench.py's headline
-# measurement (`bench.py --only`: the timed graph replay over input sets twice the last-level
-# cache), whose last 200 dispatches are the timed ones. FA_FORCE_BR / FA_FORCE_BC / FA_FORCE_SPLITS, when set,
+# measurement (`bench.py --only`: three timed loops of host-issued launches over input sets twice
+# the last-level cache), whose last 200 dispatches are the last timed loop. FA_FORCE_BR / FA_FORCE_BC / FA_FORCE_SPLITS, when set,
 # pass through to the library and are recorded with the commands.
 #
 # Passes, each its own rocprofv3 run under its own time limit (counters never share a run with a
