@@ -452,7 +452,7 @@ int launch_s3(const KArgs& in, hipStream_t stream) {
 
 template <typename T, int D, int WAVES, int BC>
 constexpr Variant variant_s3() {
-  return Variant{D, 32 * WAVES, BC, &launch_s3<T, D, WAVES, BC>};
+  return Variant{D, 32 * WAVES, BC, &launch_s3<T, D, WAVES, BC>, WAVES};
 }
 
 // Stage 3: BR fixed at 128, BC in {32, 64}.

@@ -1016,7 +1016,7 @@ int launch(const KArgs& in, hipStream_t stream) {
 
 template <int STAGE, typename T, int D, int RG, int KS, int BCW>
 constexpr Variant variant() {
-  return Variant{D, 32 * RG, KS * BCW, &launch<STAGE, T, D, RG, KS, BCW>};
+  return Variant{D, 32 * RG, KS * BCW, &launch<STAGE, T, D, RG, KS, BCW>, RG * KS};
 }
 
 // ---- instantiation tables: one (RG, KS, BCW) per (BR, BC) -------------------------------------
@@ -1033,15 +1033,17 @@ struct S5Rows {
       variant<STAGE, T, D, 1, 2, 32>(),  // BR  32, BC  64 (2-way split)
       variant<STAGE, T, D, 2, 1, 32>(),  // BR  64, BC  32
       variant<STAGE, T, D, 2, 2, 32>(),  // BR  64, BC  64 (2-way split)
-      variant<STAGE, T, D, 2, 2, 64>(),  // BR  64, BC 128 (2-way split, 4 waves)
       variant<STAGE, T, D, 4, 1, 32>(),  // BR 128, BC  32
       variant<STAGE, T, D, 4, 2, 32>(),  // BR 128, BC  64 (2-way split) -- D = 128 default
   };
 };
 
-// At D = 64 only: BR 128 / BC 128 (4 row groups x 2 key splits of 64 keys, the D = 64 default),
-// BR 32 / BC 128 (the same waves, one row group), the height small grids are launched with, and
-// BR 256 / BC 64.
+// Per head dim, the tiles with 64 keys per wave or four key splits:
+//   D = 64:  BR 64 / 128 / 32 x BC 128 (2 key splits of 64 keys; BR 128 is the D = 64 default),
+//            BR 256 / BC 64, and BR 32 / 64 x BC 256 (4 key splits of 64 keys);
+//   D = 128: BR 32 / 64 x BC 128 (4 key splits of 32 keys).
+// The four-split tiles serve grids of at most one workgroup per CU, where two splits would leave
+// SIMDs with one wave or none.
 // STAGE 5 is the table stage 5 launches; STAGE 4 gives the same tiles with the synchronous loop
 // (launched as fa_s4_mfma), which stage 5 runs under FA_S5_PREFETCH=0.
 template <typename T, int STAGE = 5>
@@ -1050,10 +1052,13 @@ VariantList s5_table() {
   using R128 = S5Rows<T, 128, STAGE>;
   static const Variant t[] = {
       R64::rows[0],  R64::rows[1],  R64::rows[2],  R64::rows[3],
-      R64::rows[4],  R64::rows[5],  R64::rows[6],  variant<STAGE, T, 64, 8, 1, 64>(),
-      variant<STAGE, T, 64, 4, 2, 64>(),  variant<STAGE, T, 64, 1, 2, 64>(),
+      R64::rows[4],  R64::rows[5],  variant<STAGE, T, 64, 2, 2, 64>(),
+      variant<STAGE, T, 64, 8, 1, 64>(),  variant<STAGE, T, 64, 4, 2, 64>(),
+      variant<STAGE, T, 64, 1, 2, 64>(),  variant<STAGE, T, 64, 1, 4, 64>(),
+      variant<STAGE, T, 64, 2, 4, 64>(),
       R128::rows[0], R128::rows[1], R128::rows[2], R128::rows[3],
-      R128::rows[4], R128::rows[5], R128::rows[6]};
+      R128::rows[4], R128::rows[5], variant<STAGE, T, 128, 1, 4, 32>(),
+      variant<STAGE, T, 128, 2, 4, 32>()};
   return VariantList{t, static_cast<int>(sizeof(t) / sizeof(t[0]))};
 }
 

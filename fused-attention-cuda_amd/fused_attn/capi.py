@@ -29,7 +29,7 @@ DTYPE_CODES = {torch.float32: FA_DTYPE_F32, torch.float16: FA_DTYPE_F16,
 
 # Every function include/fa/attention.h declares, in declaration order.
 EXPORTS = ("fa_forward", "fa_forward_strided", "fa_workspace_bytes", "fa_impl_supports",
-           "fa_set_debug_overrides", "fa_get_debug_overrides", "fa_impl_name", "fa_dtype_name",
+           "fa_set_debug_overrides", "fa_get_debug_overrides", "fa_s5_plan", "fa_impl_name", "fa_dtype_name",
            "fa_dtype_size", "fa_current_arch", "fa_error_string", "fa_decode_num_splits",
            "fa_decode_workspace_bytes", "fa_decode", "fa_decode_noalloc")
 
@@ -87,6 +87,9 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     lib.fa_set_debug_overrides.restype = None
     lib.fa_get_debug_overrides.argtypes = [ctypes.c_bool, ctypes.POINTER(ci), ctypes.POINTER(ci)]
     lib.fa_get_debug_overrides.restype = None
+    ip = ctypes.POINTER(ci)
+    lib.fa_s5_plan.argtypes = [ci, ctypes.POINTER(FaParams), ip, ip, ip]
+    lib.fa_s5_plan.restype = ci
     lib.fa_impl_name.argtypes = [ci]
     lib.fa_impl_name.restype = ctypes.c_char_p
     lib.fa_dtype_name.argtypes = [ci]
@@ -121,6 +124,16 @@ def current_arch() -> int:
     if rc != HIP_SUCCESS:
         raise RuntimeError(f"fa_current_arch failed: {error_string(rc)}")
     return a.value
+
+
+def s5_plan(dtype: int, p: FaParams) -> tuple[int, int, int]:
+    """``fa_s5_plan``: stage 5's (BR, BC, S) for ``p`` on the current device."""
+    br, bc, s = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+    rc = load().fa_s5_plan(dtype, ctypes.byref(p), ctypes.byref(br), ctypes.byref(bc),
+                           ctypes.byref(s))
+    if rc != HIP_SUCCESS:
+        raise RuntimeError(f"fa_s5_plan failed: {error_string(rc)}")
+    return br.value, bc.value, s.value
 
 
 def error_string(rc: int) -> str:

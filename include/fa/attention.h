@@ -109,14 +109,24 @@ FA_API bool fa_impl_supports(int impl, int dtype, int D, int arch);
  * ref:src/dispatch.cu:177-189): forced query-tile height block_m (BR) and key-tile width block_n
  * (BC), 0 = kernel default. Stage 5's default height follows the grid: the tallest of 128 / 64 /
  * 32 rows that gives every compute unit a workgroup; results do not depend on it. Its default
- * width narrows (BC 64 at D = 64, BC 32 at D = 128) where several workgroups share a compute unit;
- * the width changes the order of the softmax accumulation, so results move within the stated
- * tolerance. A forced height alone keeps the automatic width where that tile is built and
+ * width narrows (BC 64 at D = 64, BC 32 at D = 128) where several workgroups share a compute unit,
+ * and doubles with twice the waves (four key splits per row group) where the grid fits one
+ * workgroup per compute unit with fewer than two waves per SIMD; the width changes the order of
+ * the softmax accumulation, so results move within the stated tolerance. A forced height alone keeps the automatic width where that tile is built and
  * otherwise takes a built width for that height, so it is valid on every grid. Process-global,
  * not thread-safe (test-only). With from_env true the environment variables FA_FORCE_BR /
  * FA_FORCE_BC override the programmatic values. */
 FA_API void fa_set_debug_overrides(int block_m, int block_n);
 FA_API void fa_get_debug_overrides(bool from_env, int* block_m, int* block_n);
+
+/* Stage 5's plan for `p` on the current device under the current overrides: the query-tile
+ * height (BR), the key-tile width (BC) and the number of key-walk parts (S, the value behind
+ * fa_workspace_bytes). Any output pointer may be null. No counterpart in the reference, whose
+ * tile height follows (D, N) alone (ref:src/stage5_tuned.cu:1011-1012); it lets callers and tests
+ * see which tile a problem runs, e.g. to force the same width at another height. Needs no device
+ * memory and launches nothing. Returns hipErrorInvalidValue for an invalid `p`, hipErrorNotSupported
+ * for fp32 (stage 5 is fp16 / bf16 only). */
+FA_API int fa_s5_plan(int dtype, const fa_params* p, int* block_m, int* block_n, int* splits);
 
 /* Replaces fa::impl_name / dtype_name / dtype_size (ref:include/fa/attention.cuh:67-69).
  * Names are the reference's: "naive", "tiled", "fused", "wmma", "tuned"; "fp32", "fp16", "bf16";

@@ -76,16 +76,21 @@ def test_stage5_split_workspace(monkeypatch):
     """Stage 5 asks for a workspace (fp32 partial O [S, B, H, N, D] + LSE [S, B, H, N]) only where
     its cost model splits the key walks. The model assumes MI355X's 256 CUs on any device (the
     size must not depend on which device is current):
-    one GPU's share of C64 over 8 GPUs (B2 H1) and of LONG (B1 H2 N8192 causal) split in two,
-    the whole benchmark shapes and the GPT-2 attention shape do not."""
+    one GPU's share of LONG over 8 GPUs (B1 H2 N8192 causal) splits in two, of C128 causal over 8
+    (B2 H1) in three, a single head of N 2048 at D 64 in four; the whole benchmark shapes, the
+    GPT-2 attention shape and C64's share over 8 GPUs (B2 H1, whose four-split tile already halves
+    the walks) do not."""
     monkeypatch.delenv("FA_FORCE_SPLITS", raising=False)
     lib = capi.load()
     f16, bf16 = capi.FA_DTYPE_F16, capi.FA_DTYPE_BF16
-    assert lib.fa_workspace_bytes(5, f16, capi.params(2, 1, 1, 2048, 64, 0.125, False)) == \
-        _split_bytes(2, 2 * 2048, 64)
     assert lib.fa_workspace_bytes(5, bf16, capi.params(1, 2, 2, 8192, 128, 0.088, True)) == \
         _split_bytes(2, 2 * 8192, 128)
-    for b, h, n, d, dt, causal in [(2, 8, 2048, 64, f16, False), (2, 8, 2048, 128, f16, False),
+    assert lib.fa_workspace_bytes(5, f16, capi.params(2, 1, 1, 2048, 128, 0.088, True)) == \
+        _split_bytes(3, 2 * 2048, 128)
+    assert lib.fa_workspace_bytes(5, f16, capi.params(1, 1, 1, 2048, 64, 0.125, False)) == \
+        _split_bytes(4, 2048, 64)
+    for b, h, n, d, dt, causal in [(2, 1, 2048, 64, f16, False), (2, 8, 2048, 64, f16, False),
+                                   (2, 8, 2048, 128, f16, False),
                                    (2, 8, 2048, 128, f16, True), (1, 16, 8192, 128, bf16, True),
                                    (1, 16, 512, 128, bf16, True), (1, 16, 1024, 128, bf16, True),
                                    (8, 12, 1024, 64, f16, True)]:
@@ -101,6 +106,54 @@ def test_stage5_split_workspace(monkeypatch):
     monkeypatch.setenv("FA_FORCE_SPLITS", "99")
     assert lib.fa_workspace_bytes(5, bf16, capi.params(1, 1, 1, 128, 128, 0.1, False)) == \
         _split_bytes(16, 128, 128)
+
+
+def test_stage5_plan(monkeypatch):
+    """fa_s5_plan names stage 5's (BR, BC, S) without a device (the CU count then reads as
+    MI355X's 256): the benchmark shapes' tiles, the four-split tiles of small grids, forced tiles,
+    and the same S as fa_workspace_bytes; invalid params and fp32 are refused."""
+    for var in ("FA_FORCE_BR", "FA_FORCE_BC", "FA_FORCE_SPLITS"):
+        monkeypatch.delenv(var, raising=False)
+    lib = capi.load()
+    lib.fa_set_debug_overrides(0, 0)
+    f16, bf16 = capi.FA_DTYPE_F16, capi.FA_DTYPE_BF16
+    cases = [((2, 8, 2048, 64, False), f16, (128, 128, 1)),   # C64
+             ((2, 8, 2048, 128, False), f16, (128, 64, 1)),   # C128
+             ((2, 8, 2048, 64, True), f16, (64, 128, 1)),     # C64 causal
+             ((8, 12, 1024, 64, True), f16, (64, 64, 1)),     # GPT-2 attention
+             ((1, 16, 8192, 128, True), bf16, (128, 32, 1)),  # LONG
+             ((1, 16, 512, 128, True), bf16, (32, 128, 1)),   # four splits, BR 32
+             ((1, 16, 1024, 128, True), bf16, (64, 128, 1)),  # four splits, BR 64
+             ((1, 8, 2048, 64, False), f16, (64, 256, 1)),    # four splits at D = 64
+             ((2, 1, 2048, 64, True), f16, (32, 256, 1)),     # four splits instead of S = 2
+             ((1, 2, 8192, 128, True), bf16, (64, 64, 2))]    # S = 2: four splits would not fit
+    for (b, h, n, d, causal), dt, plan in cases:
+        p = capi.params(b, h, h, n, d, 0.1, causal)
+        assert capi.s5_plan(dt, p) == plan, (b, h, n, d, causal)
+        s = plan[2]
+        want = 0 if s == 1 else _split_bytes(s, b * h * n, d)
+        assert lib.fa_workspace_bytes(5, dt, p) == want
+    p = capi.params(1, 16, 16, 512, 128, 0.1, True)
+    lib.fa_set_debug_overrides(128, 0)   # no BR 128 tile of the four-split width: BC 64
+    assert capi.s5_plan(bf16, p)[:2] == (128, 64)
+    lib.fa_set_debug_overrides(64, 0)    # BR 64 keeps the automatic width
+    assert capi.s5_plan(bf16, p)[:2] == (64, 128)
+    lib.fa_set_debug_overrides(0, 32)    # a forced width takes the height rule
+    assert capi.s5_plan(bf16, p)[:2] == (32, 32)
+    monkeypatch.setenv("FA_FORCE_BR", "64")
+    monkeypatch.setenv("FA_FORCE_BC", "64")
+    assert capi.s5_plan(bf16, p)[:2] == (64, 64)
+    lib.fa_set_debug_overrides(0, 0)
+    monkeypatch.delenv("FA_FORCE_BR")
+    monkeypatch.delenv("FA_FORCE_BC")
+    out = ctypes.c_int(-1)
+    assert lib.fa_s5_plan(f16, ctypes.byref(p), None, ctypes.byref(out), None) == capi.HIP_SUCCESS
+    assert out.value == 128
+    bad = capi.params(1, 16, 16, 500, 128, 0.1, True)
+    assert lib.fa_s5_plan(f16, ctypes.byref(bad), None, None, None) == capi.HIP_ERROR_INVALID_VALUE
+    assert lib.fa_s5_plan(f16, None, None, None, None) == capi.HIP_ERROR_INVALID_VALUE
+    assert lib.fa_s5_plan(capi.FA_DTYPE_F32, ctypes.byref(p), None, None, None) == \
+        capi.HIP_ERROR_NOT_SUPPORTED
 
 
 def test_impl_supports_registry():

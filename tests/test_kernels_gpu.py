@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import fused_attn
+from fused_attn import capi
 from _checks import ABS_CAP, LSE_ATOL, LSE_TOL_REF, O_TOL, assert_close_tol, \
     assert_every_head_close, check_against_reference
 from oracle.oracle import error_ratio, math_reference, unfused_reference
@@ -31,8 +32,8 @@ STAGE_DTYPE_PAIRS = [(s, dt) for s in (3, 4, 5) for dt in STAGE_DTYPES[s]]
 # Instantiated (BR, BC) tiles per stage (csrc/attn_mfma16.h and csrc/attn_kernel.h tables;
 # 0 = default). Stages 3 and 4 fix BR at 128 and ignore a forced BR, as the reference's S3/S4 do.
 STAGE_BC = {3: {32, 64}, 4: {32, 64, 128}}
-S5_TILES = {(32, 32), (32, 64), (32, 128), (64, 32), (64, 64), (64, 128), (128, 32), (128, 64),
-            (128, 128), (256, 64)}
+S5_TILES = {(32, 32), (32, 64), (32, 128), (32, 256), (64, 32), (64, 64), (64, 128), (64, 256),
+            (128, 32), (128, 64), (128, 128), (256, 64)}
 S5_DEFAULT = (128, 128)  # at D = 64, the head dim of the tile tests
 
 _ids = {torch.float32: "fp32", torch.float16: "fp16", torch.bfloat16: "bf16"}
@@ -94,9 +95,12 @@ def test_stage5_full_tile_counts(n, d, dtype, make_qkv):
 
 # Stage 5 picks its workgroup height from the grid when no BR is forced: the tallest of 128 / 64 /
 # 32 rows that still gives every compute unit a workgroup. Each 32-row wave runs the same key split
-# and key order at every height, so the default must equal every forced height bit for bit. The
-# shapes are small grids (the default is BR 32 or 64 there) with N an odd multiple of 32, so the
-# forced BR = 64 / 128 runs also cover partial query tiles.
+# and key order at every height, so the default must equal every forced height that keeps the
+# default width bit for bit (fa_s5_plan names the width a forced height gets: a height with no tile
+# of the default width, such as BR 128 beside a four-split default, takes another width and is
+# checked against the oracle instead). The shapes are small grids (the default is BR 32 or 64
+# there) with N an odd multiple of 32, so the forced BR = 64 / 128 runs also cover partial query
+# tiles.
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 @pytest.mark.parametrize("b,h,n,d", [(1, 3, 96, 64), (2, 4, 224, 64), (1, 16, 512, 128),
                                      (2, 3, 352, 128)], ids=lambda x: str(x))
@@ -105,15 +109,27 @@ def test_stage5_default_height_matches_forced_heights(b, h, n, d, dtype, causal,
                                                       reset_overrides):
     require(5, dtype, d)
     q, k, v = make_qkv(b, h, n, d, dtype=dtype, device="cuda", seed=5)
+    code = capi.DTYPE_CODES[dtype]
+    p = capi.params(b, h, h, n, d, d ** -0.5, causal)
     fused_attn.set_debug_overrides(0, 0)
+    _, bc0, _ = capi.s5_plan(code, p)
     o0, lse0 = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
     check_against_reference(o0, q, k, v, causal, dtype, lse=lse0)
+    same_width = 0
     for br in (128, 64, 32):
         fused_attn.set_debug_overrides(br, 0)
+        assert capi.s5_plan(code, p)[0] == br
+        bc = capi.s5_plan(code, p)[1]
         o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
         torch.cuda.synchronize()
-        assert torch.equal(o, o0) and torch.equal(lse, lse0), f"BR = {br} differs from the default"
+        if bc == bc0:
+            same_width += 1
+            assert torch.equal(o, o0) and torch.equal(lse, lse0), \
+                f"BR = {br} (BC {bc}) differs from the default"
+        else:
+            check_against_reference(o, q, k, v, causal, dtype, lse=lse)
     fused_attn.set_debug_overrides(0, 0)
+    assert same_width >= 2, "fewer than two heights keep the default width"
 
 
 # The tile stage 5 picks by itself on grids that fill a 256-CU device (csrc/dispatch.cpp,
@@ -154,6 +170,42 @@ def test_stage5_automatic_tile_on_full_grids(b, h, n, d, dtype, causal, tile, ma
     # Every head of the grid against the fp32 reference: a tile rule that mixed up heads,
     # query tiles or key splits anywhere would show here.
     assert_every_head_close(o0, lse0, q, k, v, causal, d ** -0.5, what=f"tile {tile}")
+
+
+# Grids of at most one workgroup per CU whose two-split tile would leave a SIMD with one wave take
+# the tile of twice the width and twice the waves at the same height: four key splits of 32 keys
+# (D = 128) or 64 keys (D = 64) per row group. Compared with the forced tile bit for bit, every head
+# against the fp32 reference, and with the two-split tile of the same height within twice the bar.
+@pytest.mark.parametrize("b,h,n,d,dtype,causal,tile,two", [
+    (1, 16, 512, 128, torch.bfloat16, True, (32, 128), (32, 64)),    # LONG_N512
+    (1, 16, 1024, 128, torch.bfloat16, True, (64, 128), (64, 64)),   # LONG_N1024
+    (1, 16, 1024, 128, torch.bfloat16, False, (64, 128), (64, 64)),  # LONG_ring8
+    (1, 8, 2048, 64, torch.float16, False, (64, 256), (64, 128)),    # D = 64
+    (2, 1, 2048, 64, torch.float16, True, (32, 256), (32, 128)),     # C64 / 8 GPUs, causal
+    (1, 3, 544, 128, torch.float16, True, (32, 128), (32, 64)),      # ragged last key tile
+], ids=["long-n512", "long-n1024", "ring8", "d64", "d64-causal-heads", "ragged"])
+def test_stage5_four_split_tile_on_small_grids(b, h, n, d, dtype, causal, tile, two, make_qkv,
+                                              reset_overrides):
+    require(5, dtype, d)
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the expected tiles are those of a 256-CU device")
+    p = capi.params(b, h, h, n, d, d ** -0.5, causal)
+    fused_attn.set_debug_overrides(0, 0)
+    assert capi.s5_plan(capi.DTYPE_CODES[dtype], p)[:2] == tile
+    q, k, v = make_qkv(b, h, n, d, dtype=dtype, device="cuda", seed=13)
+    o0, lse0 = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
+    fused_attn.set_debug_overrides(*tile)
+    o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
+    fused_attn.set_debug_overrides(*two)
+    o2, _ = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
+    fused_attn.set_debug_overrides(0, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o0) and torch.equal(lse, lse0), f"the default is not {tile}"
+    assert_every_head_close(o0, lse0, q, k, v, causal, d ** -0.5, what=f"tile {tile}")
+    atol, rtol = O_TOL[dtype]
+    base = o2.double()
+    excess = float(((o0.double() - base).abs() - 2 * (atol + rtol * base.abs())).max())
+    assert excess <= 0.0, f"four splits differ from two by more than twice the bar ({excess})"
 
 
 @pytest.mark.parametrize("stage", [1, 2])

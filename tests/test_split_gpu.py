@@ -82,9 +82,10 @@ def test_more_parts_than_key_tiles(dtype, monkeypatch):
 
 
 @pytest.mark.parametrize("b,h,n,d,dtype,causal", [
-    (2, 1, 2048, 64, torch.float16, False),    # C64 over 8 GPUs by heads
-    (1, 2, 4096, 128, torch.bfloat16, True),   # a LONG-like share by heads (N halved)
-], ids=["C64-heads8", "long-heads"])
+    (2, 1, 2048, 128, torch.float16, True),    # C128 causal over 8 GPUs by heads: 3 parts
+    (1, 2, 8192, 128, torch.bfloat16, True),   # LONG over 8 GPUs by heads: 2 parts
+    (1, 1, 2048, 64, torch.float16, False),    # one head at D = 64: 4 parts
+], ids=["C128-causal-heads8", "long-heads8", "one-head-d64"])
 def test_model_splits_share_shapes(b, h, n, d, dtype, causal, monkeypatch):
     _require()
     monkeypatch.delenv("FA_FORCE_SPLITS", raising=False)
