@@ -53,8 +53,11 @@ struct Dec16 {
   // The decode's LDS: F's double-buffered K/V tiles, reused for the key-split merge at the end.
   // (F's own kLdsBytes also counts the Q region of the forward's prologue, which the decode, with
   // its query rows in registers, does not have.)
-  static constexpr size_t kLdsBytes =
-      F::kTileBytes > F::kMergeBytes ? F::kTileBytes : F::kMergeBytes;
+  // Merge scratch: each of the three non-leading key splits writes its O^T registers, m and l
+  // per lane.
+  static constexpr int kMergeFloats = (F::kDB * 16 + 2) * 64;
+  static constexpr size_t kMergeBytes = static_cast<size_t>(3) * RG * kMergeFloats * sizeof(float);
+  static constexpr size_t kLdsBytes = F::kTileBytes > kMergeBytes ? F::kTileBytes : kMergeBytes;
   static constexpr int BC = F::BC;        // 128 keys per tile
   static constexpr int kWaves = F::kWaves;
   static constexpr int kThreads = F::kThreads;
@@ -174,7 +177,7 @@ struct Dec16 {
     // barrier).
     float* mg = reinterpret_cast<float*>(lds_raw);
     if (ksp > 0) {
-      float* dst = mg + ((ksp - 1) * RG + rg) * F::kMergeFloats;
+      float* dst = mg + ((ksp - 1) * RG + rg) * kMergeFloats;
 #pragma unroll
       for (int db = 0; db < kDB; ++db) {
 #pragma unroll
@@ -187,7 +190,7 @@ struct Dec16 {
     if (ksp > 0) return;
 #pragma unroll
     for (int sp = 1; sp < 4; ++sp) {
-      const float* src = mg + ((sp - 1) * RG + rg) * F::kMergeFloats;
+      const float* src = mg + ((sp - 1) * RG + rg) * kMergeFloats;
       const float m1 = src[kDB * 16 * 64 + lane];
       const float l1 = src[(kDB * 16 + 1) * 64 + lane];
       const float m_new = fmaxf(ws.m, m1);

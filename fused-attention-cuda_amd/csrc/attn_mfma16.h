@@ -156,12 +156,25 @@ struct Fa16 {
   static constexpr int kChunks = BC * kRowChunks;  // per tensor and tile
   static constexpr int kDmaInsts = kChunks / 64;   // 1 KiB LDS-DMA instructions per tensor/tile
   static constexpr int kDmaPerWave = kDmaInsts / kWaves;
-  // Merge scratch: every non-leading key split writes its O^T registers, m and l per lane.
-  static constexpr int kMergeFloats = (kDB * 16 + 2) * 64;
+  // Merge and epilogue (run() after the key walk). The O^T accumulator of a wave is kGroups groups
+  // of 4 registers; group gi = 4 db + j holds head-dim entries 32 db + 8 j + 4 (lane / 32) + 0..3
+  // of the lane's row. The KS waves of a row group split the groups: wave ks finishes the kOwn
+  // groups [ks kOwn, (ks + 1) kOwn), a contiguous slice of kSliceD head-dim entries.
+  static constexpr int kGroups = kDB * 4;
+  static constexpr int kOwn = kGroups / KS;
+  static constexpr int kSliceD = kOwn * 8;
+  // Merge scratch: every wave writes the groups the other waves finish (KS - 1 slices of 1 KiB per
+  // group), then m and l per lane.
+  static constexpr size_t kPartBytes =
+      static_cast<size_t>(KS - 1) * RG * KS * kOwn * 64 * 16;
   static constexpr size_t kMergeBytes =
-      KS > 1 ? static_cast<size_t>(KS - 1) * RG * kMergeFloats * sizeof(float) : 0;
+      KS > 1 ? kPartBytes + static_cast<size_t>(KS) * RG * 64 * 8 : 0;
+  // Output staging: 32 rows of the wave's slice, each padded by 16 bytes.
+  static constexpr int kStageRow = kSliceD + 8;  // elements
+  static constexpr size_t kStageBytes = static_cast<size_t>(RG) * KS * 32 * kStageRow * 2;
+  static constexpr size_t kEpiBytes = kMergeBytes > kStageBytes ? kMergeBytes : kStageBytes;
   static constexpr size_t kLdsBytes =
-      kTileBytes + kQBytes > kMergeBytes ? kTileBytes + kQBytes : kMergeBytes;
+      kTileBytes + kQBytes > kEpiBytes ? kTileBytes + kQBytes : kEpiBytes;
   // fp16 fast path: p = exp2(s c - m c) is used as long as every probability of the tile stays
   // <= 2^14 (so the fp16 operand, max 65504, cannot overflow); the check is the lane's tile row
   // sum, which bounds each of its probabilities.
@@ -175,6 +188,9 @@ struct Fa16 {
   static_assert(kDmaInsts % kWaves == 0, "every wave issues the same number of DMA instructions");
   static_assert(kBr * D / 8 % (64 * kWaves) == 0, "the Q tile is whole DMA instructions per wave");
   static_assert(2 * kDmaPerWave < 64, "prologue vmcnt immediates fit 6 bits");
+  static_assert(kGroups % KS == 0 && kOwn % 2 == 0, "whole, even slices of O^T groups per wave");
+  static_assert(KS == 1 || 32 * kStageRow * 2 <= kOwn * 64 * 16,
+                "a wave's staging fits its slice of one other wave's merge scratch");
 
   // LDS layout of a K/V tile (layout::swz): BC rows of D elements, unpadded, with the 16-byte
   // chunks of each row XOR-swizzled by a function of the row chosen by measured read rate.
@@ -788,89 +804,126 @@ struct Fa16 {
     }
 
     // ---- merge the KS partial states of each row group (LDS is free after the last barrier) ----
+    // Each wave finishes its slice of the head dim: m_fin = max_s m_s, w_s = exp2((m_s - m_fin) c),
+    // O = sum_s w_s O_s and l = sum_s w_s l_s (the log-sum-exp merge of partial softmax states,
+    // ref:include/fa/softmax_math.cuh:65-68; a split that saw no key of the row has m_s = -inf
+    // and weighs nothing).
+    auto group = [&](int gi) __attribute__((always_inline)) {
+      return float4{ws.o[gi / 4][4 * (gi % 4) + 0], ws.o[gi / 4][4 * (gi % 4) + 1],
+                    ws.o[gi / 4][4 * (gi % 4) + 2], ws.o[gi / 4][4 * (gi % 4) + 3]};
+    };
+    float4 own[kOwn];
+    float m_fin, lt;
+    T* stage;  // this wave's output staging: 32 rows of kStageRow elements
     if constexpr (KS > 1) {
-      float* mg = reinterpret_cast<float*>(lds_raw);
-      if (ks > 0) {
-        float* dst = mg + ((ks - 1) * RG + rg) * kMergeFloats;
+      // Scratch: source s writes the groups of every other wave's slice, compacted (group gi at
+      // gi - kOwn past its own slice), [s][rg][kGroups - kOwn][64 lanes] float4; then (m, l) per
+      // [s][rg][lane].
+      float4* const parts = reinterpret_cast<float4*>(lds_raw);
+      float2* const mls = reinterpret_cast<float2*>(lds_raw + kPartBytes);
+      auto part_at = [&](int src, int gi) {  // gi outside src's own slice
+        return parts + ((src * RG + rg) * (kGroups - kOwn) + gi - (gi >= src * kOwn ? kOwn : 0)) * 64 +
+               lane;
+      };
 #pragma unroll
-        for (int db = 0; db < kDB; ++db) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) dst[(db * 16 + r) * 64 + lane] = ws.o[db][r];
-        }
-        dst[kDB * 16 * 64 + lane] = ws.m;
-        dst[(kDB * 16 + 1) * 64 + lane] = ws.l;
+      for (int gi = 0; gi < kGroups; ++gi) {
+        if (gi / kOwn != ks) *part_at(ks, gi) = group(gi);
       }
+      mls[(ks * RG + rg) * 64 + lane] = float2{ws.m, ws.l};
       __syncthreads();
-      if (ks > 0) return;
+      float ms[KS], ls[KS];
+      m_fin = -__builtin_inff();
 #pragma unroll
-      for (int sp = 1; sp < KS; ++sp) {
-        const float* src = mg + ((sp - 1) * RG + rg) * kMergeFloats;
-        const float m1 = src[kDB * 16 * 64 + lane];
-        const float l1 = src[(kDB * 16 + 1) * 64 + lane];
-        const float m_new = fmaxf(ws.m, m1);
-        const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
-        const float a0 = exp2_hw((ws.m - m_use) * c);
-        const float a1 = exp2_hw((m1 - m_use) * c);
-        ws.l = ws.l * a0 + l1 * a1;
-#pragma unroll
-        for (int db = 0; db < kDB; ++db) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            ws.o[db][r] = ws.o[db][r] * a0 + src[(db * 16 + r) * 64 + lane] * a1;
-          }
-        }
-        ws.m = m_new;
+      for (int sp = 0; sp < KS; ++sp) {
+        const float2 x = mls[(sp * RG + rg) * 64 + lane];
+        ms[sp] = x.x;
+        ls[sp] = x.y;
+        m_fin = fmaxf(m_fin, x.x);
       }
+      const float m_use = (m_fin == -__builtin_inff()) ? 0.f : m_fin;
+      // Explicit fused multiply-adds, in split order: every tile height rounds a row the same way.
+      float lsum = 0.f;
+#pragma unroll
+      for (int q = 0; q < kOwn; ++q) own[q] = float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int sp = 0; sp < KS; ++sp) {
+        const float w = exp2_hw((ms[sp] - m_use) * c);
+        lsum = __builtin_fmaf(ls[sp], w, lsum);
+#pragma unroll
+        for (int q = 0; q < kOwn; ++q) {
+          float4 x;
+          if (sp == ks) {
+            x = group(q);
+#pragma unroll
+            for (int kk = 1; kk < KS; ++kk) {
+              if (ks == kk) x = group(kk * kOwn + q);
+            }
+          } else {
+            x = *part_at(sp, ks * kOwn + q);
+          }
+          own[q] = float4{__builtin_fmaf(x.x, w, own[q].x), __builtin_fmaf(x.y, w, own[q].y),
+                          __builtin_fmaf(x.z, w, own[q].z), __builtin_fmaf(x.w, w, own[q].w)};
+        }
+      }
+      lt = halves_sum(lsum);
+      // Staging: this wave's slice in the scratch of source 0 (1 if this is wave 0), which no other
+      // wave reads; the reads above were issued first, and one wave's LDS operations complete in
+      // order.
+      stage = reinterpret_cast<T*>(part_at(ks == 0 ? 1 : 0, ks * kOwn) - lane);
+    } else {
+#pragma unroll
+      for (int q = 0; q < kOwn; ++q) own[q] = group(q);
+      m_fin = ws.m;
+      lt = halves_sum(ws.l);
+      stage = reinterpret_cast<T*>(lds_raw) + static_cast<size_t>(wave) * 32 * kStageRow;
     }
 
     // ---- epilogue: O = acc / l, lse = m*scale + ln l (ref:include/fa/softmax_math.cuh:58-71) ----
-    const float lt = halves_sum(ws.l);
     if (!wave_valid) return;
     const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
+    const int d0 = ks * kSliceD;  // first head-dim entry of this wave's slice
     if (S > 1) {
       // One part of a split walk: its normalised O in fp32 and its LSE (-inf when the part saw
       // no key) for fa_s5_combine.
       const size_t prow =
           ((static_cast<size_t>(part) * a.B + b) * a.H + h) * static_cast<size_t>(N) + row;
-      float* op = a.o_part + prow * D;
+      float* op = a.o_part + prow * D + d0;
 #pragma unroll
-      for (int db = 0; db < kDB; ++db) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int d = 32 * db + 8 * j + 4 * g;
-          *reinterpret_cast<float4*>(op + d) =
-              float4{ws.o[db][4 * j + 0] * inv, ws.o[db][4 * j + 1] * inv,
-                     ws.o[db][4 * j + 2] * inv, ws.o[db][4 * j + 3] * inv};
-        }
+      for (int q = 0; q < kOwn; ++q) {
+        *reinterpret_cast<float4*>(op + 8 * q + 4 * g) = own[q] * inv;
       }
-      if (g == 0) {
-        a.lse_part[prow] = (lt > 0.f && ws.m != -__builtin_inff())
-                               ? ws.m * a.scale + log2_hw(lt) * kLn2
+      if (ks == 0 && g == 0) {
+        a.lse_part[prow] = (lt > 0.f && m_fin != -__builtin_inff())
+                               ? m_fin * a.scale + log2_hw(lt) * kLn2
                                : -__builtin_inff();
       }
       return;
     }
-    T* orow = static_cast<T*>(a.o) + b * a.osb + h * a.osh + row * a.osn;
+    // Through LDS to whole-row stores: lane (row, g) writes its 4 entries of each group, then every
+    // lane stores 16 contiguous bytes, consecutive lanes along a row's slice.
 #pragma unroll
-    for (int db = 0; db < kDB; ++db) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d = 32 * db + 8 * j + 4 * g;
-        const float x0 = ws.o[db][4 * j + 0] * inv, x1 = ws.o[db][4 * j + 1] * inv;
-        const float x2 = ws.o[db][4 * j + 2] * inv, x3 = ws.o[db][4 * j + 3] * inv;
-        if constexpr (kF16) {
-          *reinterpret_cast<f16x4*>(orow + d) =
-              f16x4{(_Float16)x0, (_Float16)x1, (_Float16)x2, (_Float16)x3};
-        } else {
-          *reinterpret_cast<bf16x4*>(orow + d) =
-              bf16x4{(__bf16)x0, (__bf16)x1, (__bf16)x2, (__bf16)x3};
-        }
+    for (int q = 0; q < kOwn; ++q) {
+      const float4 x = own[q] * inv;
+      T* dst = stage + (lane & 31) * kStageRow + 8 * q + 4 * g;
+      if constexpr (kF16) {
+        *reinterpret_cast<f16x4*>(dst) =
+            f16x4{(_Float16)x.x, (_Float16)x.y, (_Float16)x.z, (_Float16)x.w};
+      } else {
+        *reinterpret_cast<bf16x4*>(dst) = bf16x4{(__bf16)x.x, (__bf16)x.y, (__bf16)x.z, (__bf16)x.w};
       }
     }
-    if (g == 0) {
+    T* const obase = static_cast<T*>(a.o) + b * a.osb + h * a.osh + r0 * a.osn + d0;
+#pragma unroll
+    for (int i = 0; i < kOwn / 2; ++i) {
+      const int ch = i * 64 + lane;
+      const int r = ch / kOwn, cc = ch % kOwn;
+      *reinterpret_cast<u32x4*>(obase + r * a.osn + 8 * cc) =
+          *reinterpret_cast<const u32x4*>(stage + r * kStageRow + 8 * cc);
+    }
+    if (ks == 0 && g == 0) {
       a.lse[(static_cast<size_t>(b) * a.H + h) * static_cast<size_t>(N) + row] =
-          (lt > 0.f && ws.m != -__builtin_inff()) ? ws.m * a.scale + log2_hw(lt) * kLn2
-                                                   : __builtin_inff();
+          (lt > 0.f && m_fin != -__builtin_inff()) ? m_fin * a.scale + log2_hw(lt) * kLn2
+                                                    : __builtin_inff();
     }
   }
 };
