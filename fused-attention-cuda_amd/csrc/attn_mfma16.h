@@ -900,7 +900,10 @@ struct Fa16 {
       return;
     }
     // Through LDS to whole-row stores: lane (row, g) writes its 4 entries of each group, then every
-    // lane stores 16 contiguous bytes, consecutive lanes along a row's slice.
+    // lane stores 16 contiguous bytes, consecutive lanes along a row's slice. The stores are
+    // non-temporal: nothing in this launch reads O, and rows written whole need no merging in L2
+    // (measured against plain stores on cache-cold inputs: C128 -1.9 %, C128 causal -2.9 %, LONG
+    // at N 512 -4.5 %, C64 and LONG unchanged).
 #pragma unroll
     for (int q = 0; q < kOwn; ++q) {
       const float4 x = own[q] * inv;
@@ -917,8 +920,8 @@ struct Fa16 {
     for (int i = 0; i < kOwn / 2; ++i) {
       const int ch = i * 64 + lane;
       const int r = ch / kOwn, cc = ch % kOwn;
-      *reinterpret_cast<u32x4*>(obase + r * a.osn + 8 * cc) =
-          *reinterpret_cast<const u32x4*>(stage + r * kStageRow + 8 * cc);
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(stage + r * kStageRow + 8 * cc),
+                                  reinterpret_cast<u32x4*>(obase + r * a.osn + 8 * cc));
     }
     if (ks == 0 && g == 0) {
       a.lse[(static_cast<size_t>(b) * a.H + h) * static_cast<size_t>(N) + row] =
