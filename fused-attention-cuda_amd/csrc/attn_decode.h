@@ -53,10 +53,12 @@ struct Dec16 {
   // The decode's LDS: F's double-buffered K/V tiles, reused for the key-split merge at the end.
   // (F's own kLdsBytes also counts the Q region of the forward's prologue, which the decode, with
   // its query rows in registers, does not have.)
-  // Merge scratch: each of the three non-leading key splits writes its O^T registers, m and l
-  // per lane.
-  static constexpr int kMergeFloats = (F::kDB * 16 + 2) * 64;
-  static constexpr size_t kMergeBytes = static_cast<size_t>(3) * RG * kMergeFloats * sizeof(float);
+  // Merge scratch: each key split's wave writes the three slices of its O^T registers that the
+  // other splits finish (kGroups - kOwn groups of 4 registers, 1 KiB each), then m and l per lane.
+  static constexpr int kGroups = F::kDB * 4;
+  static constexpr int kOwn = kGroups / 4;
+  static constexpr size_t kPartBytes = static_cast<size_t>(4) * RG * (kGroups - kOwn) * 64 * 16;
+  static constexpr size_t kMergeBytes = kPartBytes + static_cast<size_t>(4) * RG * 64 * 8;
   static constexpr size_t kLdsBytes = F::kTileBytes > kMergeBytes ? F::kTileBytes : kMergeBytes;
   static constexpr int BC = F::BC;        // 128 keys per tile
   static constexpr int kWaves = F::kWaves;
@@ -174,77 +176,93 @@ struct Dec16 {
     }
 
     // Merge the four key splits' partial states of each row group (LDS is free after the last
-    // barrier).
-    float* mg = reinterpret_cast<float*>(lds_raw);
-    if (ksp > 0) {
-      float* dst = mg + ((ksp - 1) * RG + rg) * kMergeFloats;
+    // barrier), in parallel: the O accumulator's head-dim entries are cut into four slices of
+    // kOwn 4-register groups, each split's wave writes the other three slices to LDS, and after
+    // one barrier wave ksp merges slice ksp of all four splits: m* = max m_s,
+    // w_s = exp2((m_s - m*) c), O = sum_s w_s O_s, l = sum_s w_s l_s, with explicit fused
+    // multiply-adds in split order.
+    auto group = [&](int gi) __attribute__((always_inline)) {
+      return float4{ws.o[gi / 4][4 * (gi % 4) + 0], ws.o[gi / 4][4 * (gi % 4) + 1],
+                    ws.o[gi / 4][4 * (gi % 4) + 2], ws.o[gi / 4][4 * (gi % 4) + 3]};
+    };
+    float4* const parts = reinterpret_cast<float4*>(lds_raw);
+    float2* const mls = reinterpret_cast<float2*>(lds_raw + kPartBytes);
+    auto part_at = [&](int src, int gi) {  // gi outside src's own slice
+      return parts + ((src * RG + rg) * (kGroups - kOwn) + gi - (gi >= src * kOwn ? kOwn : 0)) * 64 +
+             lane;
+    };
 #pragma unroll
-      for (int db = 0; db < kDB; ++db) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) dst[(db * 16 + r) * 64 + lane] = ws.o[db][r];
-      }
-      dst[kDB * 16 * 64 + lane] = ws.m;
-      dst[(kDB * 16 + 1) * 64 + lane] = ws.l;
+    for (int gi = 0; gi < kGroups; ++gi) {
+      if (gi / kOwn != ksp) *part_at(ksp, gi) = group(gi);
     }
+    mls[(ksp * RG + rg) * 64 + lane] = float2{ws.m, ws.l};
     __syncthreads();
-    if (ksp > 0) return;
+    float ms[4], ls[4];
+    float m_fin = -__builtin_inff();
 #pragma unroll
-    for (int sp = 1; sp < 4; ++sp) {
-      const float* src = mg + ((sp - 1) * RG + rg) * kMergeFloats;
-      const float m1 = src[kDB * 16 * 64 + lane];
-      const float l1 = src[(kDB * 16 + 1) * 64 + lane];
-      const float m_new = fmaxf(ws.m, m1);
-      const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;
-      const float a0 = exp2_hw((ws.m - m_use) * c);
-      const float a1 = exp2_hw((m1 - m_use) * c);
-      ws.l = ws.l * a0 + l1 * a1;
-#pragma unroll
-      for (int db = 0; db < kDB; ++db) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) ws.o[db][r] = ws.o[db][r] * a0 + src[(db * 16 + r) * 64 + lane] * a1;
-      }
-      ws.m = m_new;
+    for (int sp = 0; sp < 4; ++sp) {
+      const float2 x = mls[(sp * RG + rg) * 64 + lane];
+      ms[sp] = x.x;
+      ls[sp] = x.y;
+      m_fin = fmaxf(m_fin, x.x);
     }
-    const float lt = halves_sum(ws.l);
+    const float m_use = (m_fin == -__builtin_inff()) ? 0.f : m_fin;
+    float lsum = 0.f;
+    float4 own[kOwn];
+#pragma unroll
+    for (int q = 0; q < kOwn; ++q) own[q] = float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sp = 0; sp < 4; ++sp) {
+      const float w = exp2_hw((ms[sp] - m_use) * c);
+      lsum = __builtin_fmaf(ls[sp], w, lsum);
+#pragma unroll
+      for (int q = 0; q < kOwn; ++q) {
+        float4 x;
+        if (sp == ksp) {
+          x = group(q);
+#pragma unroll
+          for (int kk = 1; kk < 4; ++kk) {
+            if (ksp == kk) x = group(kk * kOwn + q);
+          }
+        } else {
+          x = *part_at(sp, ksp * kOwn + q);
+        }
+        own[q] = float4{__builtin_fmaf(x.x, w, own[q].x), __builtin_fmaf(x.y, w, own[q].y),
+                        __builtin_fmaf(x.z, w, own[q].z), __builtin_fmaf(x.w, w, own[q].w)};
+      }
+    }
+    const float lt = halves_sum(lsum);
     if (!row_valid) return;
-    const bool empty = !(lt > 0.f) || ws.m == -__builtin_inff();
+    const bool empty = !(lt > 0.f) || m_fin == -__builtin_inff();
     const float inv = empty ? 0.f : 1.f / lt;
     // lse of the split: m*scale + ln(l); an empty split reports -inf so the combine ignores it,
     // and with a single split the final convention (+inf for a row with no key) applies.
     const float lse = empty ? (a.S == 1 ? __builtin_inff() : -__builtin_inff())
-                            : ws.m * a.scale + log2_hw(lt) * kLn2;
+                            : m_fin * a.scale + log2_hw(lt) * kLn2;
+    const int d0 = ksp * kOwn * 8;  // first head-dim entry of this wave's slice
     if (a.S == 1) {
-      T* orow = static_cast<T*>(a.o) + static_cast<size_t>(q0 + row) * D;
+      T* orow = static_cast<T*>(a.o) + static_cast<size_t>(q0 + row) * D + d0;
 #pragma unroll
-      for (int db = 0; db < kDB; ++db) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int d = 32 * db + 8 * j + 4 * g;
-          const float x0 = ws.o[db][4 * j + 0] * inv, x1 = ws.o[db][4 * j + 1] * inv;
-          const float x2 = ws.o[db][4 * j + 2] * inv, x3 = ws.o[db][4 * j + 3] * inv;
-          if constexpr (F::kF16) {
-            *reinterpret_cast<f16x4*>(orow + d) = f16x4{(_Float16)x0, (_Float16)x1, (_Float16)x2, (_Float16)x3};
-          } else {
-            *reinterpret_cast<bf16x4*>(orow + d) = bf16x4{(__bf16)x0, (__bf16)x1, (__bf16)x2, (__bf16)x3};
-          }
+      for (int q = 0; q < kOwn; ++q) {
+        const float4 x = own[q] * inv;
+        if constexpr (F::kF16) {
+          *reinterpret_cast<f16x4*>(orow + 8 * q + 4 * g) =
+              f16x4{(_Float16)x.x, (_Float16)x.y, (_Float16)x.z, (_Float16)x.w};
+        } else {
+          *reinterpret_cast<bf16x4*>(orow + 8 * q + 4 * g) =
+              bf16x4{(__bf16)x.x, (__bf16)x.y, (__bf16)x.z, (__bf16)x.w};
         }
       }
-      if (g == 0) a.lse[q0 + row] = lse;
+      if (ksp == 0 && g == 0) a.lse[q0 + row] = lse;
     } else {
       // Partials: o_part [B, Hkv, S, R, D] and lse_part [B, Hkv, S, R], fp32.
       const size_t pr = (static_cast<size_t>(b * a.Hkv + hkv) * a.S + s) * a.R + row;
-      float* orow = a.o_part + pr * D;
+      float* orow = a.o_part + pr * D + d0;
 #pragma unroll
-      for (int db = 0; db < kDB; ++db) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int d = 32 * db + 8 * j + 4 * g;
-          *reinterpret_cast<float4*>(orow + d) =
-              float4{ws.o[db][4 * j] * inv, ws.o[db][4 * j + 1] * inv, ws.o[db][4 * j + 2] * inv,
-                     ws.o[db][4 * j + 3] * inv};
-        }
+      for (int q = 0; q < kOwn; ++q) {
+        *reinterpret_cast<float4*>(orow + 8 * q + 4 * g) = own[q] * inv;
       }
-      if (g == 0) a.lse_part[pr] = lse;
+      if (ksp == 0 && g == 0) a.lse_part[pr] = lse;
     }
   }
 };
