@@ -711,7 +711,11 @@ def main(argv=None) -> int:
         line["configs_protocol"] = (
             "ms: host-issued launches over rotating input sets that together are twice the "
             "256 MB last-level cache (cold_sets), median of three loops, as `value`; warm_ms: the "
-            "same over 4 cache-resident sets")
+            "same over 4 cache-resident sets; gate_max_err_o / gate_max_err_lse: before timing, "
+            "rows 0-31 and N-32..N-1 of two heads against the fp64 oracle must meet |O err| <= "
+            "2e-3 + 2e-3 |ref| and |LSE err| <= 1e-3 (every dtype here; the parity tests hold "
+            "bf16 to 2e-3 + 2^-8 |ref|, bf16's own unit roundoff being 2^-8 > 2e-3, and fp32 to "
+            "1e-5)")
         # Tile skipping: causal over dense time at the two canonical head dims (the reference
         # reports 1.64-1.86x for its stage 5, ref:docs/STAGES.md:644-652; 2x is the ideal).
         line["causal_speedup"] = {

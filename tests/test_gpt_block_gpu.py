@@ -30,13 +30,15 @@ def test_strided_and_dense_fused_blocks_agree_bitwise():
     assert torch.equal(y_strided, y_dense)
 
 
-def test_block_attention_matches_fp32_attention():
+@pytest.mark.parametrize("batch", [2, 8], ids=["b2", "b8-config5"])
+def test_block_attention_matches_fp32_attention(batch):
     """The attention output inside the block (fp16 kernel) against fp32 torch attention on the
-    same q, k, v, to the fp16 bar of the dense parity tests."""
+    same q, k, v, to the fp16 bar of the dense parity tests; batch 8 is BASELINE config 5's
+    timed block (T 1024, 12 heads of 64)."""
     require_ext()
     model = gpt_block.build("fused", seed=4)
     attn = model.block.attn
-    idx = gpt_block.token_ids(2, 1024, seed=2)
+    idx = gpt_block.token_ids(batch, 1024, seed=2)
     with torch.no_grad():
         x = model.block.ln_1(model.wte(idx) + model.wpe(torch.arange(1024, device="cuda")))
         qkv = attn.c_attn(x)
