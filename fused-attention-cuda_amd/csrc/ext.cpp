@@ -1,14 +1,15 @@
-// ext.cpp -- fused_attn._C: the PyTorch-ROCm custom-op binding over the C-ABI of libfa_hip.so.
+// ext.cpp -- fused_attn._C: the torch.ops.fused_attn.* custom ops over the C-ABI of libfa_hip.so.
 //
-// Mirrors the reference binding (ref:python/fused_attn/ext.cpp): the same TORCH_LIBRARY schemas
-// (ref:python/fused_attn/ext.cpp:220-230), the same input contract checks and error messages
-// (:82-126), the same stage selection (:171-188) and the same (O, LSE) allocation (:129-169). The
-// kernels are reached only through include/fa/attention.h (fa_forward & co.), i.e. this file is a
-// consumer of the C-ABI exactly as any other FFI would be. Host C++ only.
+// The op surface is the reference's (ref:python/fused_attn/ext.cpp): its TORCH_LIBRARY schemas
+// (:220-230), its input contract with the same messages and the same order of checks (:82-126),
+// forward running the highest implemented stage (:171-188), and (O, LSE) outputs from the caching
+// allocator (:129-169). Below that surface the file is a plain client of include/fa/attention.h:
+// the kernels are reached through fa_forward / fa_forward_strided / fa_decode only, as any other
+// FFI would reach them. Host C++ only.
 //
-// ROCm PyTorch tensors carry the CUDA dispatch key and device type, so the kernels are
-// registered for `CUDA`, and the device guard / current stream come from the HIP
-// "masquerading as CUDA" helpers.
+// ROCm PyTorch tensors carry the CUDA dispatch key and device type, so the kernels are registered
+// for `CUDA`, and the device guard and current stream come from the HIP "masquerading as CUDA"
+// helpers.
 #include <Python.h>  // first, per the CPython docs
 // (this comment ends the include block so formatters keep Python.h first)
 
@@ -30,145 +31,187 @@
 
 namespace {
 
-constexpr int64_t kMinStage = 1;
-constexpr int64_t kMaxStage = 5;
-// Stages whose kernels write the logsumexp; 1-2 would return an empty lse (CONTRACT section 4 of
-// the reference, ref:python/fused_attn/ext.cpp:43-45).
-constexpr int64_t kFirstLseStage = 3;
+// ---- codes ---------------------------------------------------------------------------------------
 
-int to_fa_dtype(at::ScalarType t) {
-  if (t == at::kFloat) return FA_DTYPE_F32;
-  if (t == at::kHalf) return FA_DTYPE_F16;
-  TORCH_CHECK(t == at::kBFloat16, "fused_attn: unsupported dtype ", t,
-              " (supported: float32, float16, bfloat16)");
-  return FA_DTYPE_BF16;
+// The stage ladder: 1 (naive) .. 5 (tuned). Stages from 3 on write the logsumexp; below that the
+// op returns an empty lse (the reference's CONTRACT section 4).
+constexpr int64_t kLowestStage = 1;
+constexpr int64_t kHighestStage = 5;
+constexpr int64_t kFirstStageWithLse = 3;
+
+constexpr std::array<int, 3> kDtypeCodes = {FA_DTYPE_F32, FA_DTYPE_F16, FA_DTYPE_BF16};
+
+int dtype_code(at::ScalarType t) {
+  switch (t) {
+    case at::kFloat:
+      return FA_DTYPE_F32;
+    case at::kHalf:
+      return FA_DTYPE_F16;
+    case at::kBFloat16:
+      return FA_DTYPE_BF16;
+    default:
+      TORCH_CHECK(false, "fused_attn: unsupported dtype ", t,
+                  " (supported: float32, float16, bfloat16)");
+  }
+  return -1;
 }
 
-int dtype_from_name(const std::string& name) {
-  if (name == "fp32") return FA_DTYPE_F32;
-  if (name == "fp16") return FA_DTYPE_F16;
-  TORCH_CHECK(name == "bf16", "fused_attn: unknown dtype name '", name,
-              "' (expected fp32, fp16 or bf16)");
-  return FA_DTYPE_BF16;
+// The library's own names ("fp32", "fp16", "bf16") are the op's dtype strings.
+int dtype_code(const std::string& name) {
+  for (const int code : kDtypeCodes) {
+    if (name == fa_dtype_name(code)) return code;
+  }
+  TORCH_CHECK(false, "fused_attn: unknown dtype name '", name, "' (expected fp32, fp16 or bf16)");
+  return -1;
 }
 
-// gfx number of the CURRENT device (950 for MI355X), the encoding fa_impl_supports() expects.
-// Callers make the right device current with a guard first.
-int current_arch() {
-  int arch = 0;
-  const int rc = fa_current_arch(&arch);
-  TORCH_CHECK(rc == 0, "fused_attn: cannot query the device architecture: ", fa_error_string(rc));
-  return arch;
+void require_stage(int64_t stage) {
+  TORCH_CHECK(stage >= kLowestStage && stage <= kHighestStage,
+              "fused_attn: stage must be in 1..5, got ", stage);
 }
 
-void check_stage(int64_t stage) {
-  TORCH_CHECK(stage >= kMinStage && stage <= kMaxStage, "fused_attn: stage must be in 1..5, got ",
-              stage);
+// A size or count of the op as the C-ABI's int.
+int as_int(int64_t value, const char* name) {
+  TORCH_CHECK(value >= 0 && value <= std::numeric_limits<int>::max(), "fused_attn: ", name, "=",
+              value, " does not fit fa_params (int)");
+  return static_cast<int>(value);
 }
 
-int checked_int(int64_t v, const char* what) {
-  TORCH_CHECK(v >= 0 && v <= std::numeric_limits<int>::max(), "fused_attn: ", what, "=", v,
-              " does not fit fa_params (int)");
-  return static_cast<int>(v);
-}
+// ---- the input contract -------------------------------------------------------------------------
 
-// The frozen input contract; every violation is a RuntimeError with a message, never a device
-// fault (ref:python/fused_attn/ext.cpp:82-126). `dense` is the reference's contiguity rule;
-// forward_strided relaxes it to a contiguous head dim with 16-byte-aligned strides.
-fa_params make_params(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
-                      bool is_causal, double scale, bool dense = true) {
-  TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(),
+// The q, k, v of one call. `views`: forward_strided's relaxed layout rule (a contiguous head dim
+// and 16-byte-multiple strides) instead of the op's dense [B, H, N, D].
+struct Operands {
+  const at::Tensor& q;
+  const at::Tensor& k;
+  const at::Tensor& v;
+  bool views;
+
+  std::array<const at::Tensor*, 3> each() const { return {&q, &k, &v}; }
+};
+
+// The contract as a list of rules, checked in the reference's order: the first broken rule is the
+// error a caller sees. Every rule raises a RuntimeError with its message; none lets a bad operand
+// reach a kernel.
+using Rule = void (*)(const Operands&);
+
+void on_one_device(const Operands& x) {
+  TORCH_CHECK(x.q.is_cuda() && x.k.is_cuda() && x.v.is_cuda(),
               "fused_attn: q, k, v must be CUDA (ROCm/HIP device) tensors");
-  TORCH_CHECK(q.device() == k.device() && q.device() == v.device(),
+  TORCH_CHECK(x.q.device() == x.k.device() && x.q.device() == x.v.device(),
               "fused_attn: q, k, v must live on the same device");
-  TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4,
-              "fused_attn: q, k, v must be [B, H, N, D]; got ", q.dim(), "-D, ", k.dim(), "-D, ",
-              v.dim(), "-D");
-  if (dense) {
-    TORCH_CHECK(q.is_contiguous() && k.is_contiguous() && v.is_contiguous(),
+}
+
+void four_dims(const Operands& x) {
+  TORCH_CHECK(x.q.dim() == 4 && x.k.dim() == 4 && x.v.dim() == 4,
+              "fused_attn: q, k, v must be [B, H, N, D]; got ", x.q.dim(), "-D, ", x.k.dim(),
+              "-D, ", x.v.dim(), "-D");
+}
+
+void readable_layout(const Operands& x) {
+  if (!x.views) {
+    TORCH_CHECK(x.q.is_contiguous() && x.k.is_contiguous() && x.v.is_contiguous(),
                 "fused_attn: q, k, v must be contiguous [B, H, N, D] (call .contiguous())");
-  } else {
-    for (const at::Tensor* t : {&q, &k, &v}) {
-      TORCH_CHECK(t->stride(3) == 1 || t->size(3) == 1,
-                  "fused_attn: forward_strided needs a contiguous head dim (stride(-1) == 1)");
-      const int64_t per16 = 16 / static_cast<int64_t>(t->element_size());
-      for (int d = 0; d < 3; ++d) {
-        TORCH_CHECK(t->stride(d) >= 0 && t->stride(d) % per16 == 0,
-                    "fused_attn: forward_strided needs batch/head/row strides that are multiples "
-                    "of 16 bytes, got stride(", d, ")=", t->stride(d));
-      }
+    return;
+  }
+  for (const at::Tensor* t : x.each()) {
+    TORCH_CHECK(t->stride(3) == 1 || t->size(3) == 1,
+                "fused_attn: forward_strided needs a contiguous head dim (stride(-1) == 1)");
+    const int64_t per16 = 16 / static_cast<int64_t>(t->element_size());
+    for (int d = 0; d < 3; ++d) {
+      TORCH_CHECK(t->stride(d) >= 0 && t->stride(d) % per16 == 0,
+                  "fused_attn: forward_strided needs batch/head/row strides that are multiples "
+                  "of 16 bytes, got stride(", d, ")=", t->stride(d));
     }
   }
-  // The kernels use 16-byte vector loads; a contiguous offset view such as t[2:] is not 16-byte
-  // aligned and is refused here rather than faulting inside the kernel.
-  for (const at::Tensor* t : {&q, &k, &v}) {
+}
+
+// The kernels read 16 bytes at a time: an offset view such as t[2:] is refused here instead of
+// faulting in the kernel.
+void aligned_bases(const Operands& x) {
+  for (const at::Tensor* t : x.each()) {
     TORCH_CHECK(reinterpret_cast<std::uintptr_t>(t->data_ptr()) % 16 == 0,
                 "fused_attn: q/k/v must be 16-byte aligned (use a fresh contiguous tensor)");
   }
-  TORCH_CHECK(q.scalar_type() == k.scalar_type() && q.scalar_type() == v.scalar_type(),
-              "fused_attn: q, k, v must share one dtype; got ", q.scalar_type(), ", ",
-              k.scalar_type(), ", ", v.scalar_type());
-  (void)to_fa_dtype(q.scalar_type());
+}
 
-  const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
-  const int64_t Hkv = k.size(1);
-  TORCH_CHECK(k.size(0) == B && v.size(0) == B, "fused_attn: batch mismatch between q, k, v");
-  TORCH_CHECK(v.size(1) == Hkv, "fused_attn: k and v must have the same number of heads");
-  TORCH_CHECK(k.size(2) == N && v.size(2) == N,
-              "fused_attn: Nq == Nkv is required (got Nq=", N, ", Nkv=", k.size(2), ")");
-  TORCH_CHECK(k.size(3) == D && v.size(3) == D, "fused_attn: head-dim mismatch between q, k, v");
+void one_dtype(const Operands& x) {
+  TORCH_CHECK(x.q.scalar_type() == x.k.scalar_type() && x.q.scalar_type() == x.v.scalar_type(),
+              "fused_attn: q, k, v must share one dtype; got ", x.q.scalar_type(), ", ",
+              x.k.scalar_type(), ", ", x.v.scalar_type());
+  (void)dtype_code(x.q.scalar_type());
+}
+
+void matching_shapes(const Operands& x) {
+  const int64_t B = x.q.size(0), H = x.q.size(1), N = x.q.size(2), D = x.q.size(3);
+  const int64_t Hkv = x.k.size(1);
+  TORCH_CHECK(x.k.size(0) == B && x.v.size(0) == B, "fused_attn: batch mismatch between q, k, v");
+  TORCH_CHECK(x.v.size(1) == Hkv, "fused_attn: k and v must have the same number of heads");
+  TORCH_CHECK(x.k.size(2) == N && x.v.size(2) == N,
+              "fused_attn: Nq == Nkv is required (got Nq=", N, ", Nkv=", x.k.size(2), ")");
+  TORCH_CHECK(x.k.size(3) == D && x.v.size(3) == D,
+              "fused_attn: head-dim mismatch between q, k, v");
   TORCH_CHECK(D == 64 || D == 128, "fused_attn: D must be 64 or 128, got ", D);
   TORCH_CHECK(N % 32 == 0, "fused_attn: N must be a multiple of 32, got ", N,
               " (ragged sequence lengths are a stated limitation)");
   TORCH_CHECK(Hkv >= 1 && H % Hkv == 0, "fused_attn: H=", H, " must be a multiple of Hkv=", Hkv);
+}
 
+constexpr std::array<Rule, 6> kContract = {on_one_device, four_dims,  readable_layout,
+                                           aligned_bases, one_dtype, matching_shapes};
+
+// fa_params of a call that keeps the contract.
+fa_params params_of(const Operands& x, bool is_causal, double scale) {
+  for (const Rule rule : kContract) rule(x);
   fa_params p;
-  p.B = checked_int(B, "B");
-  p.H = checked_int(H, "H");
-  p.Hkv = checked_int(Hkv, "Hkv");
-  p.N = checked_int(N, "N");
-  p.D = checked_int(D, "D");
+  p.B = as_int(x.q.size(0), "B");
+  p.H = as_int(x.q.size(1), "H");
+  p.Hkv = as_int(x.k.size(1), "Hkv");
+  p.N = as_int(x.q.size(2), "N");
+  p.D = as_int(x.q.size(3), "D");
   p.scale = static_cast<float>(scale);
   p.causal = is_causal;
   return p;
 }
 
-// Runs one explicit stage; returns (o, lse), lse empty for stages < 3
-// (ref:python/fused_attn/ext.cpp:128-169).
-std::tuple<at::Tensor, at::Tensor> run_stage(const at::Tensor& q, const at::Tensor& k,
-                                             const at::Tensor& v, bool is_causal, double scale,
-                                             int64_t stage) {
-  check_stage(stage);
-  const fa_params p = make_params(q, k, v, is_causal, scale);
-  const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-  const int impl = static_cast<int>(stage);
-  const int dtype = to_fa_dtype(q.scalar_type());
-  const int arch = current_arch();
-  TORCH_CHECK(fa_impl_supports(impl, dtype, p.D, arch), "fused_attn: stage ", stage, " (",
-              fa_impl_name(impl), ") is not implemented for ", fa_dtype_name(dtype), " D=", p.D,
-              " on gfx", arch);
+// ---- launching ----------------------------------------------------------------------------------
 
-  at::Tensor o = at::empty_like(q);
-  const bool has_lse = stage >= kFirstLseStage;
-  at::Tensor lse = has_lse ? at::empty({p.B, p.H, p.N}, q.options().dtype(at::kFloat))
-                           : at::empty({0}, q.options().dtype(at::kFloat));
-  // Scratch for the materialising stages, and stage 5's optional workspace where it splits key
-  // walks (0 bytes otherwise); freed stream-ordered by the caching allocator after the
-  // asynchronous launch.
-  const size_t ws_bytes = fa_workspace_bytes(impl, dtype, &p);
-  at::Tensor workspace;
-  void* ws_ptr = nullptr;
-  if (ws_bytes > 0) {
-    workspace = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
-    ws_ptr = workspace.data_ptr();
+// q's device made current for the rest of the call (the stream, the arch query and every
+// allocation follow it), with its architecture and current stream.
+struct DeviceScope {
+  explicit DeviceScope(const at::Tensor& q)
+      : guard(q.device()),
+        stream(c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.device().index()).stream()) {
+    const int rc = fa_current_arch(&arch);
+    TORCH_CHECK(rc == 0, "fused_attn: cannot query the device architecture: ", fa_error_string(rc));
   }
-  const hipStream_t stream =
-      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.device().index()).stream();
-  const int err = fa_forward(impl, dtype, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                             has_lse ? lse.data_ptr<float>() : nullptr, ws_ptr, &p, stream);
-  TORCH_CHECK(err == 0, "fused_attn: stage ", stage, " (", fa_impl_name(impl),
-              ") failed: ", fa_error_string(err));
-  return std::make_tuple(std::move(o), std::move(lse));
+  c10::hip::HIPGuardMasqueradingAsCUDA guard;
+  hipStream_t stream;
+  int arch = 0;
+};
+
+// The highest stage implemented for (dtype, D) on `arch`, 0 if none.
+int highest_stage(int dtype, int D, int arch) {
+  for (int64_t s = kHighestStage; s >= kLowestStage; --s) {
+    if (fa_impl_supports(static_cast<int>(s), dtype, D, arch)) return static_cast<int>(s);
+  }
+  return 0;
+}
+
+// A byte tensor of the size fa_workspace_bytes asks for (undefined when it asks for none): the
+// materialising stages' scratch, or stage 5's optional split-walk workspace. Released by the
+// caching allocator in stream order after the asynchronous launch.
+at::Tensor workspace_for(int stage, int dtype, const fa_params& p, const at::Tensor& like) {
+  const size_t bytes = fa_workspace_bytes(stage, dtype, &p);
+  if (bytes == 0) return at::Tensor();
+  return at::empty({static_cast<int64_t>(bytes)}, like.options().dtype(at::kByte));
+}
+
+void* data_or_null(const at::Tensor& t) { return t.defined() ? t.data_ptr() : nullptr; }
+
+void check_launched(int status, int stage) {
+  TORCH_CHECK(status == 0, "fused_attn: stage ", stage, " (", fa_impl_name(stage),
+              ") failed: ", fa_error_string(status));
 }
 
 fa_strides strides_of(const at::Tensor& t) {
@@ -179,9 +222,9 @@ fa_strides strides_of(const at::Tensor& t) {
   return s;
 }
 
-// A dense tensor with q's shape whose memory order follows q's strides (outermost first): for
-// the [B, H, N, D] view of a [B, N, H, D] buffer the result is a [B, N, H, D] buffer seen as
-// [B, H, N, D], so the caller's transpose back to [B, N, H*D] is free. Contiguous q gives a
+// A dense tensor with q's shape whose memory order follows q's strides (outermost first): for the
+// [B, H, N, D] view of a [B, N, H, D] buffer the result is a [B, N, H, D] buffer seen as
+// [B, H, N, D], so a caller's transpose back to [B, N, H*D] is free. A contiguous q gives a
 // contiguous result. ops.py's fake kernel applies the same rule.
 at::Tensor empty_in_layout_of(const at::Tensor& q) {
   std::array<int64_t, 4> order = {0, 1, 2, 3};
@@ -195,68 +238,74 @@ at::Tensor empty_in_layout_of(const at::Tensor& q) {
   return at::empty(sizes, q.options()).permute(inverse);
 }
 
-// forward_strided: as forward (best stage, O only) over strided views (fa_forward_strided). No
-// counterpart in the reference (its op requires dense tensors); it removes the layout copies
-// around the op in a transformer block.
-at::Tensor forward_strided_cuda(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
-                                bool is_causal, double scale) {
-  const fa_params p = make_params(q, k, v, is_causal, scale, /*dense=*/false);
-  const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-  const int dtype = to_fa_dtype(q.scalar_type());
-  const int arch = current_arch();
-  int stage = 0;
-  for (int s = static_cast<int>(kMaxStage); s >= static_cast<int>(kMinStage) && stage == 0; --s) {
-    if (fa_impl_supports(s, dtype, p.D, arch)) stage = s;
-  }
-  TORCH_CHECK(stage >= kFirstLseStage, "fused_attn: no stage is implemented for ",
-              fa_dtype_name(dtype), " D=", p.D, " on gfx", arch);
-  at::Tensor o = empty_in_layout_of(q);
-  at::Tensor lse = at::empty({p.B, p.H, p.N}, q.options().dtype(at::kFloat));
-  const fa_strides qs = strides_of(q), ks = strides_of(k), vs = strides_of(v), os = strides_of(o);
-  // Stage 5's optional workspace (split key walks), as in forward.
-  const size_t ws_bytes = fa_workspace_bytes(stage, dtype, &p);
-  at::Tensor workspace;
-  if (ws_bytes > 0) {
-    workspace = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
-  }
-  const hipStream_t stream =
-      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.device().index()).stream();
-  const int err = fa_forward_strided(stage, dtype, q.data_ptr(), &qs, k.data_ptr(), &ks,
-                                     v.data_ptr(), &vs, o.data_ptr(), &os, lse.data_ptr<float>(),
-                                     ws_bytes > 0 ? workspace.data_ptr() : nullptr, &p, stream);
-  TORCH_CHECK(err == 0, "fused_attn: stage ", stage, " (", fa_impl_name(stage),
-              ") failed: ", fa_error_string(err));
-  return o;
-}
+// ---- the ops ------------------------------------------------------------------------------------
 
-// forward: the highest implemented stage for (dtype, D, arch) (ref:python/fused_attn/ext.cpp:171-188).
-at::Tensor forward_cuda(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
-                        bool is_causal, double scale) {
-  const fa_params p = make_params(q, k, v, is_causal, scale);
-  const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-  const int dtype = to_fa_dtype(q.scalar_type());
-  const int arch = current_arch();
-  for (int64_t stage = kMaxStage; stage >= kMinStage; --stage) {
-    if (fa_impl_supports(static_cast<int>(stage), dtype, p.D, arch)) {
-      return std::get<0>(run_stage(q, k, v, is_causal, scale, stage));
-    }
-  }
-  TORCH_CHECK(false, "fused_attn: no stage is implemented for ", fa_dtype_name(dtype), " D=", p.D,
-              " on gfx", arch);
-  return at::Tensor();
-}
-
+// forward_stage: one explicit stage; (o, lse), lse empty below stage 3.
 std::tuple<at::Tensor, at::Tensor> forward_stage_cuda(const at::Tensor& q, const at::Tensor& k,
                                                       const at::Tensor& v, bool is_causal,
                                                       double scale, int64_t stage) {
-  return run_stage(q, k, v, is_causal, scale, stage);
+  require_stage(stage);
+  const fa_params p = params_of(Operands{q, k, v, false}, is_causal, scale);
+  const DeviceScope dev(q);
+  const int impl = static_cast<int>(stage);
+  const int dtype = dtype_code(q.scalar_type());
+  TORCH_CHECK(fa_impl_supports(impl, dtype, p.D, dev.arch), "fused_attn: stage ", stage, " (",
+              fa_impl_name(impl), ") is not implemented for ", fa_dtype_name(dtype), " D=", p.D,
+              " on gfx", dev.arch);
+  at::Tensor o = at::empty_like(q);
+  const auto f32 = q.options().dtype(at::kFloat);
+  at::Tensor lse = stage >= kFirstStageWithLse ? at::empty({p.B, p.H, p.N}, f32) : at::empty({0}, f32);
+  const at::Tensor ws = workspace_for(impl, dtype, p, q);
+  check_launched(fa_forward(impl, dtype, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                            stage >= kFirstStageWithLse ? lse.data_ptr<float>() : nullptr,
+                            data_or_null(ws), &p, dev.stream),
+                 impl);
+  return std::make_tuple(std::move(o), std::move(lse));
+}
+
+// forward: the highest implemented stage for (dtype, D, arch); O only.
+at::Tensor forward_cuda(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                        bool is_causal, double scale) {
+  const fa_params p = params_of(Operands{q, k, v, false}, is_causal, scale);
+  const int dtype = dtype_code(q.scalar_type());
+  int stage = 0, arch = 0;
+  {
+    const DeviceScope dev(q);
+    arch = dev.arch;
+    stage = highest_stage(dtype, p.D, arch);
+  }
+  TORCH_CHECK(stage != 0, "fused_attn: no stage is implemented for ", fa_dtype_name(dtype), " D=",
+              p.D, " on gfx", arch);
+  return std::get<0>(forward_stage_cuda(q, k, v, is_causal, scale, stage));
+}
+
+// forward_strided: forward over strided [B, H, N, D] views (fa_forward_strided), read in place;
+// O comes back dense in q's memory order. No counterpart in the reference (its op takes dense
+// tensors); it removes the layout copies around the op in a transformer block.
+at::Tensor forward_strided_cuda(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                bool is_causal, double scale) {
+  const fa_params p = params_of(Operands{q, k, v, true}, is_causal, scale);
+  const DeviceScope dev(q);
+  const int dtype = dtype_code(q.scalar_type());
+  const int stage = highest_stage(dtype, p.D, dev.arch);
+  TORCH_CHECK(stage >= kFirstStageWithLse, "fused_attn: no stage is implemented for ",
+              fa_dtype_name(dtype), " D=", p.D, " on gfx", dev.arch);
+  at::Tensor o = empty_in_layout_of(q);
+  at::Tensor lse = at::empty({p.B, p.H, p.N}, q.options().dtype(at::kFloat));
+  const std::array<fa_strides, 4> st = {strides_of(q), strides_of(k), strides_of(v),
+                                        strides_of(o)};
+  const at::Tensor ws = workspace_for(stage, dtype, p, q);
+  check_launched(fa_forward_strided(stage, dtype, q.data_ptr(), &st[0], k.data_ptr(), &st[1],
+                                    v.data_ptr(), &st[2], o.data_ptr(), &st[3],
+                                    lse.data_ptr<float>(), data_or_null(ws), &p, dev.stream),
+                 stage);
+  return o;
 }
 
 // decode: split-KV decode (fa_decode). q [B, H, Nq, D]; k, v [B, Hkv, Nkv, D]; returns
 // (o [B, H, Nq, D], lse [B, H, Nq] fp32). No counterpart in the reference's op (its stated next
-// step, ref:README.md:1357-1358). The workspace is a byte tensor from the caching allocator,
-// released in stream order like the reference's stage workspace
-// (ref:python/fused_attn/ext.cpp:143-157).
+// step, ref:README.md:1357-1358). The split partials live in a byte tensor from the caching
+// allocator, released in stream order like the forward's workspace.
 std::tuple<at::Tensor, at::Tensor> decode_cuda(const at::Tensor& q, const at::Tensor& k,
                                                const at::Tensor& v, bool is_causal, double scale,
                                                int64_t num_splits) {
@@ -274,28 +323,26 @@ std::tuple<at::Tensor, at::Tensor> decode_cuda(const at::Tensor& q, const at::Te
   TORCH_CHECK(k.size(1) > 0 && q.size(1) % k.size(1) == 0,
               "fused_attn: H must be a multiple of Hkv");
   TORCH_CHECK(scale > 0.0, "fused_attn: scale must be > 0");
-  const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  const DeviceScope dev(q);
   fa_decode_params p{};
-  p.B = checked_int(q.size(0), "B");
-  p.H = checked_int(q.size(1), "H");
-  p.Hkv = checked_int(k.size(1), "Hkv");
-  p.Nq = checked_int(q.size(2), "Nq");
-  p.Nkv = checked_int(k.size(2), "Nkv");
-  p.D = checked_int(q.size(3), "D");
+  p.B = as_int(q.size(0), "B");
+  p.H = as_int(q.size(1), "H");
+  p.Hkv = as_int(k.size(1), "Hkv");
+  p.Nq = as_int(q.size(2), "Nq");
+  p.Nkv = as_int(k.size(2), "Nkv");
+  p.D = as_int(q.size(3), "D");
   p.scale = static_cast<float>(scale);
   p.causal = is_causal;
-  p.num_splits = checked_int(num_splits, "num_splits");
-  const int dtype = to_fa_dtype(q.scalar_type());
+  p.num_splits = as_int(num_splits, "num_splits");
+  const int dtype = dtype_code(q.scalar_type());
   at::Tensor o = at::empty_like(q);
   at::Tensor lse = at::empty({p.B, p.H, p.Nq}, q.options().dtype(at::kFloat));
   const size_t ws_bytes = fa_decode_workspace_bytes(dtype, &p);
-  at::Tensor ws;
-  if (ws_bytes > 0) ws = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
-  const hipStream_t stream =
-      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.device().index()).stream();
+  const at::Tensor ws =
+      ws_bytes > 0 ? at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte))
+                   : at::Tensor();
   const int err = fa_decode(dtype, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                            lse.data_ptr<float>(), ws_bytes > 0 ? ws.data_ptr() : nullptr, &p,
-                            stream);
+                            lse.data_ptr<float>(), data_or_null(ws), &p, dev.stream);
   TORCH_CHECK(err != static_cast<int>(hipErrorNotSupported),
               "fused_attn: decode is not implemented for ", fa_dtype_name(dtype), " D=", p.D,
               " with (H/Hkv)*Nq=", static_cast<int64_t>(p.H / p.Hkv) * p.Nq,
@@ -306,18 +353,22 @@ std::tuple<at::Tensor, at::Tensor> decode_cuda(const at::Tensor& q, const at::Te
 
 // TEST-ONLY: forces BR / BC (0 = default) for the tile-invariance tests; process-global.
 void set_debug_overrides_op(int64_t block_m, int64_t block_n) {
-  fa_set_debug_overrides(checked_int(block_m, "block_m"), checked_int(block_n, "block_n"));
+  fa_set_debug_overrides(as_int(block_m, "block_m"), as_int(block_n, "block_n"));
 }
 
 bool impl_supports_op(int64_t stage, std::string dtype, int64_t D) {
-  check_stage(stage);
+  require_stage(stage);
   if (c10::hip::device_count() == 0) return false;
-  const int dt = dtype_from_name(dtype);
-  return fa_impl_supports(static_cast<int>(stage), dt, checked_int(D, "D"), current_arch());
+  const int code = dtype_code(dtype);
+  const int d = as_int(D, "D");
+  int arch = 0;
+  const int rc = fa_current_arch(&arch);
+  TORCH_CHECK(rc == 0, "fused_attn: cannot query the device architecture: ", fa_error_string(rc));
+  return fa_impl_supports(static_cast<int>(stage), code, d, arch);
 }
 
 std::string impl_name_op(int64_t stage) {
-  check_stage(stage);
+  require_stage(stage);
   return std::string(fa_impl_name(static_cast<int>(stage)));
 }
 
