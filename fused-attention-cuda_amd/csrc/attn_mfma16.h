@@ -613,7 +613,7 @@ struct Fa16 {
     if (PIPE && a.rotate) {
       layout::rotate_walk(walk, N, BC, kBr, qt, a.causal != 0, part,
                           [&](int x) { return fdiv(x, a.fd_splits); },
-                          [&](int x) { return fdiv(x, a.fd_rot_blocks); });
+                          [&](int x) { return fdiv(x, a.fd_rot_blocks); }, a.rot_lg);
     }
     walk.rot = __builtin_amdgcn_readfirstlane(walk.rot);
     walk.rot_end = __builtin_amdgcn_readfirstlane(walk.rot_end);

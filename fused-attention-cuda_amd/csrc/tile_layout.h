@@ -118,18 +118,25 @@ FA_HD inline Walk plan_walk(int N, int BC, int BR, int qt, bool causal, int part
 // the workgroup's first row, so that every workgroup height (32, 64 or 128 rows) gives each 32-row
 // wave the same sequence of key tiles, hence the same results: the rotated range is the block's
 // steady range [t0, n_steady of a 128-row workgroup at the block), which lies inside the steady
-// range of any shorter workgroup of the block, and block blk of n_blocks starts blk / n_blocks of
-// the way round it. div_blocks(x) must return x / n_blocks, n_blocks = ceil(N / kRotRows).
+// range of any shorter workgroup of the block. With groups_lg < 0 block blk of n_blocks starts
+// blk / n_blocks of the way round it; with groups_lg = k the blocks form 2^k groups of consecutive
+// blocks, and group g = floor(blk 2^k / n_blocks) starts g / 2^k of the way round. div_blocks(x)
+// must return x / n_blocks, n_blocks = ceil(N / kRotRows).
 constexpr int kRotRows = 128;
 template <typename DivSplits, typename DivBlocks>
 FA_HD inline void rotate_walk(Walk& w, int N, int BC, int BR, int qt, bool causal, int part,
-                              DivSplits div_splits, DivBlocks div_blocks) {
+                              DivSplits div_splits, DivBlocks div_blocks, int groups_lg = -1) {
   const int blk = qt * BR / kRotRows;
   const Walk wb = plan_walk(N, BC, kRotRows, blk, causal, part, div_splits);
   const int end = wb.n_steady < w.n_steady ? wb.n_steady : w.n_steady;
   if (wb.t0 != w.t0 || end - w.t0 < 2) return;
   w.rot_end = end;
-  w.rot = div_blocks(blk * (end - w.t0));
+  if (groups_lg < 0) {
+    w.rot = div_blocks(blk * (end - w.t0));
+  } else {
+    const int g = div_blocks(blk << groups_lg);  // the block's group, 0 .. 2^groups_lg - 1
+    w.rot = (g * (end - w.t0)) >> groups_lg;
+  }
 }
 
 // The work item of workgroup `bid` of a stage-4/5 grid of G = n_qtiles * BH * splits workgroups

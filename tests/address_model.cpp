@@ -159,13 +159,13 @@ void check_q_load(const Variant& v, int N, int sn, int qt, const std::string& c)
 // The load schedule of one stage-5 (pipelined) or stage-4 (synchronous) workgroup.
 template <int D>
 void replay_workgroup(const Variant& v, int N, int sn, bool causal, int S, int part, int qt,
-                      bool pipelined, bool rotate) {
+                      bool pipelined, bool rotate, int groups_lg = -1) {
   const int BC = v.KS * v.BCW, BR = 32 * v.RG;
   auto walk = fa::layout::plan_walk(N, BC, BR, qt, causal, part, [S](int x) { return x / S; });
   const int n_blocks = (N + fa::layout::kRotRows - 1) / fa::layout::kRotRows;
   if (rotate && pipelined) {
     fa::layout::rotate_walk(walk, N, BC, BR, qt, causal, part, [S](int x) { return x / S; },
-                            [n_blocks](int x) { return x / n_blocks; });
+                            [n_blocks](int x) { return x / n_blocks; }, groups_lg);
   }
   auto wt = [&](int t) { return fa::layout::walk_tile(walk, t); };
   const std::string c = ctx(v, N, sn, causal, S, part, qt);
@@ -236,8 +236,9 @@ void sweep_variant(const Variant& v) {
         for (int S : {1, 2, 3, 5, 16}) {
           for (int part = 0; part < S; ++part) {
             for (int qt = 0; qt < n_qtiles; ++qt) {
-              for (const bool rotate : {false, true}) {
-                replay_workgroup<D>(v, N, sn, causal, S, part, qt, true, rotate);
+              replay_workgroup<D>(v, N, sn, causal, S, part, qt, true, false);
+              for (const int groups_lg : {-1, 1, 2}) {  // one start per block, 2 or 4 groups
+                replay_workgroup<D>(v, N, sn, causal, S, part, qt, true, true, groups_lg);
               }
               if (S == 1) replay_workgroup<D>(v, N, sn, causal, 1, 0, qt, false, false);
               if (S > 1) check_split_rows(N, D, S, part, qt * BR,
@@ -359,11 +360,13 @@ void check_grid_items() {
 
 }  // namespace
 
-// The rotated walk order keeps results independent of the workgroup height: every 32-row wave
-// meets the same key tiles in the same order at heights 32, 64 and 128 (the kernel computes a
-// wave's rows from its own tiles only, so equal tile sequences give equal bits). A wave's sequence
+// The rotated walk order (one start per 128-row block, or per group of blocks) keeps results
+// independent of the workgroup height: every 32-row wave meets the same key tiles in the same
+// order at heights 32, 64 and 128 (the kernel computes a wave's rows from its own tiles only, so
+// equal tile sequences give equal bits). A wave's sequence
 // is the walk order of its workgroup restricted to the tiles holding a key it can see.
 void check_rotation_height_invariance() {
+  for (const int groups_lg : {-1, 1, 2}) {
   for (int BC : {32, 64, 128}) {
     for (int N : {32, 96, 128, 224, 512, 640, 1024, 1056, 2048}) {
       for (bool causal : {false, true}) {
@@ -374,7 +377,7 @@ void check_rotation_height_invariance() {
             const int qt = r0 / BR;
             auto w = fa::layout::plan_walk(N, BC, BR, qt, causal, 0, [](int x) { return x; });
             fa::layout::rotate_walk(w, N, BC, BR, qt, causal, 0, [](int x) { return x; },
-                                    [n_blocks](int x) { return x / n_blocks; });
+                                    [n_blocks](int x) { return x / n_blocks; }, groups_lg);
             const int wave_end = causal ? (r0 + 32 < N ? r0 + 32 : N) : N;
             std::vector<int> seq;
             for (int t = w.t0; t < w.n_tiles; ++t) {
@@ -386,11 +389,13 @@ void check_rotation_height_invariance() {
           }
           if (seqs[0] != seqs[1] || seqs[0] != seqs[2]) {
             fail("rotated walk differs between heights: BC=" + std::to_string(BC) + " N=" +
-                 std::to_string(N) + (causal ? " causal" : "") + " rows " + std::to_string(r0));
+                 std::to_string(N) + (causal ? " causal" : "") + " rows " + std::to_string(r0) +
+                 " groups_lg " + std::to_string(groups_lg));
           }
         }
       }
     }
+  }
   }
 }
 

@@ -189,20 +189,30 @@ def test_gqa_splits(hkv, dtype, monkeypatch):
     (2, 2, 640, 64, torch.bfloat16, False),
 ], ids=lambda x: str(x))
 def test_rotated_and_in_order_walks_both_meet_the_oracle(b, h, n, d, dtype, causal, monkeypatch):
-    """The key walk's order (in order, or rotated per 128-row block so that workgroups sharing a
-    head fetch different tiles at a time) only reorders each row's accumulation: both orders meet
-    the fp64 oracle, forced either way with the test-only FA_FORCE_ROTATE."""
+    """The key walk's order (in order, or rotated so that workgroups sharing a head fetch different
+    tiles at a time: one start per 128-row block, or one per group of blocks) only reorders each
+    row's accumulation: every order meets the fp64 oracle, forced with the test-only
+    FA_FORCE_ROTATE and FA_FORCE_ROT_GROUPS. One group is the in-order walk again, bit for bit."""
     gen = torch.Generator().manual_seed(31)
     q, k, v = (torch.randn(b, h, n, d, generator=gen).to("cuda", dtype) for _ in range(3))
     ref, lse64 = math_reference(q, k, v, is_causal=causal)
-    outs = []
-    for force in ("0", "1"):
-        monkeypatch.setenv("FA_FORCE_ROTATE", force)
+    outs = {}
+    for rotate, groups in (("0", None), ("1", None), ("1", "1"), ("1", "2"), ("1", "4")):
+        monkeypatch.setenv("FA_FORCE_ROTATE", rotate)
+        if groups is None:
+            monkeypatch.delenv("FA_FORCE_ROT_GROUPS", raising=False)
+        else:
+            monkeypatch.setenv("FA_FORCE_ROT_GROUPS", groups)
         o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
         torch.cuda.synchronize()
+        what = f"FA_FORCE_ROTATE={rotate} FA_FORCE_ROT_GROUPS={groups}"
         err = float(abs(o.double().cpu().numpy() - ref).max())
         lerr = float(abs(lse.double().cpu().numpy() - lse64).max())
         tol = 2e-3 + (2e-3 if dtype == torch.float16 else 2 ** -8) * float(abs(ref).max())
-        assert err <= tol, f"FA_FORCE_ROTATE={force}: O error {err:.3e}"
-        assert lerr <= 1e-3, f"FA_FORCE_ROTATE={force}: LSE error {lerr:.3e}"
+        assert err <= tol, f"{what}: O error {err:.3e}"
+        assert lerr <= 1e-3, f"{what}: LSE error {lerr:.3e}"
+        outs[(rotate, groups)] = (o, lse)
+    in_order, one_group = outs[("0", None)], outs[("1", "1")]
+    assert torch.equal(in_order[0], one_group[0]) and torch.equal(in_order[1], one_group[1])
     monkeypatch.delenv("FA_FORCE_ROTATE")
+    monkeypatch.delenv("FA_FORCE_ROT_GROUPS", raising=False)
