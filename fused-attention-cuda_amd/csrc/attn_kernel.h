@@ -32,9 +32,10 @@
 // LDS cycle).
 //
 // Work distribution: grid = (N / BR) * B * H workgroups on a 1-D grid. Hardware hands workgroup i
-// to XCD i % 8 (8 XCDs, each with its own L2); the kernel remaps blockIdx so that XCD x receives a
-// contiguous range of (head, q-tile) pairs, i.e. all Q tiles of a head sit on one XCD and its K/V
-// is fetched into one L2. For causal problems the heaviest Q tiles (longest key range) are issued
+// to XCD (i + c) % 8, c fixed for the launch (8 XCDs, each with its own L2); the kernel remaps
+// blockIdx so that the workgroups of one residue i % 8 receive a contiguous range of
+// (head, q-tile) pairs, i.e. all Q tiles of a head sit on one XCD and its K/V is fetched into one
+// L2. For causal problems the heaviest Q tiles (longest key range) are issued
 // first within each XCD.
 #pragma once
 

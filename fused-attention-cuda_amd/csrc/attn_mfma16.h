@@ -44,12 +44,13 @@
 // from HBM by global_load_lds_dwordx4 (no register staging), one contiguous KiB per wave
 // instruction; the swizzle is applied on the global side by choosing each lane's source chunk.
 //
-// Grid: 1-D, (ceil(N/BR) * B * H) workgroups. Hardware hands workgroup i to XCD i % 8 (each XCD
-// has its own L2); blockIdx is remapped so that each XCD receives a contiguous range of
-// (head, q-tile) pairs and a head's K/V is fetched into one L2 (layout::grid_item). Causal
-// problems issue the longest key ranges first, across all heads of an XCD's range when that range
-// is whole heads. Causal key tiles past the workgroup's last row are never loaded; per wave,
-// 32-key blocks past the wave's last row are skipped and only the diagonal block is masked.
+// Grid: 1-D, (ceil(N/BR) * B * H) workgroups. Hardware hands workgroup i to XCD (i + c) % 8, c
+// fixed for the launch (each XCD has its own L2); blockIdx is remapped so that each XCD receives
+// a contiguous range of (head, q-tile) pairs and a head's K/V is fetched into one L2
+// (layout::grid_item). Causal problems issue the longest key ranges first, across all heads of an
+// XCD's range when that range is whole heads. Causal key tiles past the workgroup's last row are
+// never loaded; per wave, 32-key blocks past the wave's last row are skipped and only the diagonal
+// block is masked.
 #pragma once
 
 #include <hip/hip_runtime.h>

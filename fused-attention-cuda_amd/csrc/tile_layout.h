@@ -141,8 +141,11 @@ FA_HD inline void rotate_walk(Walk& w, int N, int BC, int BR, int qt, bool causa
 
 // The work item of workgroup `bid` of a stage-4/5 grid of G = n_qtiles * BH * splits workgroups
 // (BH = B * H): its batch-head bh, query tile qt and part of a split walk. The hardware hands
-// workgroup i to XCD i % kXcds, and each XCD has its own L2, so each XCD receives a contiguous
-// range of items and fetches a head's K/V into one L2. Inside an XCD's range:
+// workgroup i to XCD (i + c) % kXcds, with c the same for every workgroup of a launch (the
+// dispatcher's round robin goes on from where earlier launches left it; XCC_ID read on the box
+// showed c = 0, 5, 6 and 7), so workgroups with equal i % kXcds share an XCD, and each XCD has its
+// own L2. Each XCD therefore receives a contiguous range of items and fetches a head's K/V into
+// one L2. Inside an XCD's range:
 //  - head-major (xcd_heads == 0): items (bh, qt, part) in order;
 //  - tile-major (xcd_heads = BH / kXcds, only when kXcds divides BH): the range is xcd_heads
 //    whole heads, issued one query tile of all of them at a time. On a causal grid that issues
