@@ -14,6 +14,9 @@ a head-sharded problem); ``FA_FORCE_SPLITS`` forces S for these tests.
   (``torch.ops.fused_attn.forward``, which allocates what ``fa_workspace_bytes`` asks for) and the
   C-ABI without a workspace (the whole-walk kernel) both match the oracle.
 * A split launch (two kernels) captured into a HIP graph replays bit-identically.
+* Walk orders: in-order and rotated walks (one start per 128-row block, or per group of blocks)
+  all meet the oracle; on the D = 64 BR x 32 tiles, rotated walks give heights 128, 64 and 32
+  the same bits, and the GPT-2 attention shape's automatic tile is that rotated walk.
 """
 
 from __future__ import annotations
@@ -216,3 +219,41 @@ def test_rotated_and_in_order_walks_both_meet_the_oracle(b, h, n, d, dtype, caus
     assert torch.equal(in_order[0], one_group[0]) and torch.equal(in_order[1], one_group[1])
     monkeypatch.delenv("FA_FORCE_ROTATE")
     monkeypatch.delenv("FA_FORCE_ROT_GROUPS", raising=False)
+
+
+@pytest.mark.parametrize("b,h,n,d,dtype,causal", [
+    (2, 4, 768, 64, torch.float16, True),
+    (1, 8, 1056, 64, torch.bfloat16, False),
+    (8, 12, 1024, 64, torch.float16, True),
+], ids=lambda x: str(x))
+def test_rotated_bc32_walks_match_across_heights(b, h, n, d, dtype, causal, monkeypatch):
+    """The D = 64 tile of one 32-key split per wave (BC 32, the automatic tile of D = 64 grids
+    with two or more BR-128 workgroups per CU, rotated up to 4 MB of K/V per XCD): with the walks
+    rotated, heights 128, 64 and 32 give every 32-row wave the same key tiles in the same order,
+    so their outputs are equal bit for bit, and they meet the fp64 oracle. The last shape is the
+    GPT-2 attention shape, which takes this tile and rotation by itself."""
+    _require()
+    gen = torch.Generator().manual_seed(37)
+    q, k, v = (torch.randn(b, h, n, d, generator=gen).to("cuda", dtype) for _ in range(3))
+    monkeypatch.setenv("FA_FORCE_ROTATE", "1")
+    monkeypatch.delenv("FA_FORCE_ROT_GROUPS", raising=False)
+    fused_attn.set_debug_overrides(0, 0)
+    p = capi.params(b, h, h, n, d, d ** -0.5, causal)
+    try:
+        outs = []
+        for br in (128, 64, 32):
+            fused_attn.set_debug_overrides(br, 32)
+            assert capi.s5_plan(capi.DTYPE_CODES[dtype], p)[:2] == (br, 32)
+            outs.append(fused_attn.forward_stage(q, k, v, 5, is_causal=causal))
+        torch.cuda.synchronize()
+    finally:
+        fused_attn.set_debug_overrides(0, 0)
+    for br, (o, lse) in zip((64, 32), outs[1:]):
+        assert torch.equal(o, outs[0][0]) and torch.equal(lse, outs[0][1]), f"BR {br} differs"
+    check_against_reference(outs[0][0], q, k, v, causal, dtype, lse=outs[0][1])
+    if (b, h, n) == (8, 12, 1024):
+        monkeypatch.delenv("FA_FORCE_ROTATE")
+        assert capi.s5_plan(capi.DTYPE_CODES[dtype], p)[:2] == (128, 32)
+        o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
+        assert torch.equal(o, outs[0][0]) and torch.equal(lse, outs[0][1]), \
+            "the automatic tile is not the rotated BR 128 x BC 32 walk"
