@@ -135,6 +135,11 @@ def test_stage5_plan(monkeypatch):
         s = plan[2]
         want = 0 if s == 1 else _split_bytes(s, b * h * n, d)
         assert lib.fa_workspace_bytes(5, dt, p) == want
+    gpt = capi.params(8, 12, 12, 1024, 64, 0.1, True)
+    lib.fa_set_debug_overrides(0, 64)    # the tall tile's height goes with its width only
+    assert capi.s5_plan(f16, gpt)[:2] == (64, 64)
+    lib.fa_set_debug_overrides(64, 0)    # a forced height keeps the tall width
+    assert capi.s5_plan(f16, gpt)[:2] == (64, 32)
     p = capi.params(1, 16, 16, 512, 128, 0.1, True)
     lib.fa_set_debug_overrides(128, 0)   # no BR 128 tile of the four-split width: BC 64
     assert capi.s5_plan(bf16, p)[:2] == (128, 64)

@@ -252,8 +252,16 @@ def test_rotated_bc32_walks_match_across_heights(b, h, n, d, dtype, causal, monk
         assert torch.equal(o, outs[0][0]) and torch.equal(lse, outs[0][1]), f"BR {br} differs"
     check_against_reference(outs[0][0], q, k, v, causal, dtype, lse=outs[0][1])
     if (b, h, n) == (8, 12, 1024):
+        # Without FA_FORCE_ROTATE: the automatic tile, and every forced height at its width,
+        # rotate by themselves (the 4 MB bound follows the width).
         monkeypatch.delenv("FA_FORCE_ROTATE")
-        assert capi.s5_plan(capi.DTYPE_CODES[dtype], p)[:2] == (128, 32)
-        o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
-        assert torch.equal(o, outs[0][0]) and torch.equal(lse, outs[0][1]), \
-            "the automatic tile is not the rotated BR 128 x BC 32 walk"
+        try:
+            for br in (0, 64, 32):
+                fused_attn.set_debug_overrides(br, 0)
+                assert capi.s5_plan(capi.DTYPE_CODES[dtype], p)[:2] == (br or 128, 32)
+                o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
+                torch.cuda.synchronize()
+                assert torch.equal(o, outs[0][0]) and torch.equal(lse, outs[0][1]), \
+                    f"BR {br or 'auto'} is not the rotated BC 32 walk"
+        finally:
+            fused_attn.set_debug_overrides(0, 0)
