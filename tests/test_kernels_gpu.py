@@ -138,9 +138,10 @@ def test_stage5_default_height_matches_forced_heights(b, h, n, d, dtype, causal,
 # B * H a multiple of 8). The height never changes results, so the comparison with the forced tile
 # pins the width; the forced tile names the height the rules pick too.
 @pytest.mark.parametrize("b,h,n,d,dtype,causal,tile", [
-    (8, 32, 1024, 64, torch.float16, False, (128, 32)),     # D = 64, N <= 2048, 8 per CU
+    (8, 32, 1024, 64, torch.float16, False, (256, 64)),     # D = 64 dense, 4 rounds of BR 256
+    (8, 12, 1024, 64, torch.float16, False, (128, 32)),     # 1.5 rounds of BR 256: tall
     (8, 12, 1024, 64, torch.float16, True, (128, 32)),      # GPT-2 attention, rotated (3 MB)
-    (2, 32, 4096, 64, torch.float16, False, (64, 64)),      # D = 64, N > 2048, 8 per CU
+    (2, 32, 4096, 64, torch.float16, True, (64, 64)),       # D = 64 causal, N > 2048, 8 per CU
     (4, 32, 512, 128, torch.float16, False, (128, 32)),     # D = 128, 2 per CU
     (4, 32, 512, 128, torch.bfloat16, True, (64, 32)),      # short causal walks
     (2, 8, 4096, 128, torch.float16, True, (128, 64)),      # causal long walks, 2 per CU
@@ -148,12 +149,12 @@ def test_stage5_default_height_matches_forced_heights(b, h, n, d, dtype, causal,
     (1, 16, 8192, 128, torch.bfloat16, True, (128, 32)),    # LONG: causal, 4 per CU
     (2, 8, 2048, 64, torch.float16, True, (64, 128)),       # C64 causal: halved height
     (2, 8, 2048, 128, torch.float16, True, (64, 64)),       # C128 causal: halved height
-    (2, 8, 4096, 64, torch.float16, False, (128, 128)),     # D = 64 long walks, 2 per CU: wide
-    (8, 8, 2048, 64, torch.float16, False, (128, 32)),      # 4 per CU, N <= 2048: tall
-    (8, 8, 2048, 64, torch.bfloat16, False, (128, 32)),     # same grid, bf16
-], ids=["d64-large", "d64-gpt2-causal", "d64-narrow", "d128-dense", "d128-short-causal",
-        "d128-causal-2cu", "d128-causal-3cu", "long", "c64-causal", "c128-causal", "d64-long-walk",
-        "d64-fp16-tall", "d64-bf16-tall"])
+    (2, 4, 4096, 64, torch.float16, False, (128, 128)),     # D = 64 long walks, 1 per CU: wide
+    (8, 8, 2048, 64, torch.float16, False, (256, 64)),      # 2 rounds of BR 256
+    (8, 8, 2048, 64, torch.bfloat16, False, (256, 64)),     # same grid, bf16
+], ids=["d64-wide256", "d64-tall-dense", "d64-gpt2-causal", "d64-narrow", "d128-dense",
+        "d128-short-causal", "d128-causal-2cu", "d128-causal-3cu", "long", "c64-causal",
+        "c128-causal", "d64-long-walk", "d64-fp16-wide256", "d64-bf16-wide256"])
 def test_stage5_automatic_tile_on_full_grids(b, h, n, d, dtype, causal, tile, make_qkv,
                                              reset_overrides):
     require(5, dtype, d)
