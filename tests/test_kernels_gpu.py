@@ -176,6 +176,30 @@ def test_stage5_automatic_tile_on_full_grids(b, h, n, d, dtype, causal, tile, ma
     assert_every_head_close(o0, lse0, q, k, v, causal, d ** -0.5, what=f"tile {tile}")
 
 
+# The D = 64 rule tiles on ragged grids: N = 1056 leaves a partial last query tile (32 of 256 or
+# 128 rows) and a partial last key tile, with and without GQA. The 256-row tile (dense, whole rounds
+# of 256-row workgroups) and the tall 128 x 32 tile (rotated where the K/V per XCD fit 4 MB) are
+# the automatic tiles here; every head is checked against the fp32 reference.
+@pytest.mark.parametrize("b,h,hkv,n,dtype,causal,tile", [
+    (16, 16, 16, 1056, torch.float16, False, (256, 64)),   # 5 rounds of BR 256
+    (16, 16, 4, 1056, torch.bfloat16, False, (256, 64)),   # GQA, 4 query heads per kv head
+    (8, 12, 12, 1056, torch.float16, True, (128, 32)),     # tall, causal, rotated (3.1 MB)
+    (8, 12, 4, 1056, torch.bfloat16, False, (128, 32)),    # tall, dense GQA (1.9 rounds of 256)
+], ids=["wide256", "wide256-gqa", "tall-causal", "tall-gqa"])
+def test_stage5_d64_rule_tiles_on_ragged_grids(b, h, hkv, n, dtype, causal, tile, make_qkv,
+                                               reset_overrides):
+    require(5, dtype, 64)
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the expected tiles are those of a 256-CU device")
+    fused_attn.set_debug_overrides(0, 0)
+    p = capi.params(b, h, hkv, n, 64, 0.125, causal)
+    assert capi.s5_plan(capi.DTYPE_CODES[dtype], p)[:2] == tile
+    q, k, v = make_qkv(b, h, n, 64, dtype=dtype, device="cuda", hkv=hkv, seed=23)
+    o, lse = fused_attn.forward_stage(q, k, v, 5, is_causal=causal)
+    torch.cuda.synchronize()
+    assert_every_head_close(o, lse, q, k, v, causal, 0.125, what=f"tile {tile}")
+
+
 # Grids of at most one workgroup per CU whose two-split tile would leave a SIMD with one wave take
 # the tile of twice the width and twice the waves at the same height: four key splits of 32 keys
 # (D = 128) or 64 keys (D = 64) per row group. Compared with the forced tile bit for bit, every head
