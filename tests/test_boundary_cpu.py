@@ -122,8 +122,10 @@ def test_stage5_plan(monkeypatch):
              ((2, 8, 2048, 64, True), f16, (64, 128, 1)),     # C64 causal
              ((8, 12, 1024, 64, True), f16, (128, 32, 1)),    # GPT-2 attention
              ((8, 12, 1024, 64, False), f16, (128, 32, 1)),   # D = 64, N <= 2048, 3 per CU
-             ((2, 32, 4096, 64, True), f16, (64, 64, 1)),     # D = 64 causal, N > 2048: narrow
+             ((3, 8, 2048, 64, True), f16, (64, 64, 1)),      # D = 64 causal, 1.5 per CU: narrow
              ((4, 8, 4096, 64, False), f16, (256, 64, 1)),    # D = 64 dense, whole rounds
+             ((2, 16, 4096, 64, True), f16, (256, 64, 1)),    # D = 64 causal N 4096, 2 rounds
+             ((1, 16, 4096, 64, True), f16, (128, 128, 1)),   # one round: wide
              ((1, 16, 8192, 128, True), bf16, (128, 32, 1)),  # LONG
              ((1, 16, 512, 128, True), bf16, (32, 128, 1)),   # four splits, BR 32
              ((1, 16, 1024, 128, True), bf16, (64, 128, 1)),  # four splits, BR 64

@@ -141,7 +141,8 @@ def test_stage5_default_height_matches_forced_heights(b, h, n, d, dtype, causal,
     (8, 32, 1024, 64, torch.float16, False, (256, 64)),     # D = 64 dense, 4 rounds of BR 256
     (8, 12, 1024, 64, torch.float16, False, (128, 32)),     # 1.5 rounds of BR 256: tall
     (8, 12, 1024, 64, torch.float16, True, (128, 32)),      # GPT-2 attention, rotated (3 MB)
-    (2, 32, 4096, 64, torch.float16, True, (64, 64)),       # D = 64 causal, N > 2048, 8 per CU
+    (3, 8, 2048, 64, torch.float16, True, (64, 64)),        # D = 64 causal, 1.5 BR-128 per CU
+    (2, 16, 4096, 64, torch.float16, True, (256, 64)),      # D = 64 causal N 4096, 2 rounds
     (4, 32, 512, 128, torch.float16, False, (128, 32)),     # D = 128, 2 per CU
     (4, 32, 512, 128, torch.bfloat16, True, (64, 32)),      # short causal walks
     (2, 8, 4096, 128, torch.float16, True, (128, 64)),      # causal long walks, 2 per CU
@@ -152,9 +153,9 @@ def test_stage5_default_height_matches_forced_heights(b, h, n, d, dtype, causal,
     (2, 4, 4096, 64, torch.float16, False, (128, 128)),     # D = 64 long walks, 1 per CU: wide
     (8, 8, 2048, 64, torch.float16, False, (256, 64)),      # 2 rounds of BR 256
     (8, 8, 2048, 64, torch.bfloat16, False, (256, 64)),     # same grid, bf16
-], ids=["d64-wide256", "d64-tall-dense", "d64-gpt2-causal", "d64-narrow", "d128-dense",
-        "d128-short-causal", "d128-causal-2cu", "d128-causal-3cu", "long", "c64-causal",
-        "c128-causal", "d64-long-walk", "d64-fp16-wide256", "d64-bf16-wide256"])
+], ids=["d64-wide256", "d64-tall-dense", "d64-gpt2-causal", "d64-narrow", "d64-wide256-causal",
+        "d128-dense", "d128-short-causal", "d128-causal-2cu", "d128-causal-3cu", "long",
+        "c64-causal", "c128-causal", "d64-long-walk", "d64-fp16-wide256", "d64-bf16-wide256"])
 def test_stage5_automatic_tile_on_full_grids(b, h, n, d, dtype, causal, tile, make_qkv,
                                              reset_overrides):
     require(5, dtype, d)
