@@ -25,7 +25,8 @@ Printed: ONE JSON line with the contract fields, plus
 * ``cpu_baseline``'s ``single_thread``: the same oracle on one thread, the reference's own loops;
 * ``configs``: the other benchmark configurations (C128, C64 and C128 causal, the long-context
   shape LONG with its N sweep 512 / 1024 / 4096 / 8192, the GPT-2 attention shape; the fp32
-  rung, stage 3, at BASELINE configs[0] -- timed beside the reference's CPU oracle on that whole
+  rung, stage 3, at the reference's CPU-runnable case (B1 H2 N128 D64 fp32) -- timed beside the
+  reference's CPU oracle on that whole
   workload -- and at C64 and C128 against the fp32 MFMA roof; stage 4 at C64 and C128), each
   timed like ``value`` (``ms``: host-issued launches over cache-cold sets, median of three) and
   over 4 cache-resident sets (``warm_ms``), plus one GPU's share of 8-GPU layouts (C64 and LONG
@@ -70,7 +71,7 @@ WORKLOADS = {
     # One GPU's share on 8 GPUs (no collective runs here): C64 and LONG split over heads (2 of
     # their 16 each), and one ring step of LONG split over the sequence instead (1024 local
     # queries against one unmasked 1024-key block).
-    # The fp32 rung (stage 3): BASELINE configs[0], the reference's CPU-runnable case, and C64 in
+    # The fp32 rung (stage 3): the reference's CPU-runnable case (B1 H2 N128 D64), and C64 in
     # fp32, against the fp32 MFMA roof.
     "CPU_cfg": (1, 2, 128, 64, "fp32", False, 1.0),
     "C64_fp32": (2, 8, 2048, 64, "fp32", False, 1.0),
@@ -692,7 +693,7 @@ def main(argv=None) -> int:
                                                    replay=False)
             res["warm_ms"] = res.pop("eager_ms")
             if name == "CPU_cfg":
-                # BASELINE configs[0] is small enough for the reference's CPU oracle to time in
+                # The reference's CPU-runnable case is small enough for its CPU oracle to time in
                 # full beside the GPU: the same workload on one host thread.
                 res["cpu_reference"] = cpu_baseline(*s2[0][:3], c2, sc2, s2[0][3], 1.0)
             # Vendor SDPA beside the fp16 configs only: its bf16 fallback path goes through

@@ -33,8 +33,8 @@ def test_strided_and_dense_fused_blocks_agree_bitwise():
 @pytest.mark.parametrize("batch", [2, 8], ids=["b2", "b8-config5"])
 def test_block_attention_matches_fp32_attention(batch):
     """The attention output inside the block (fp16 kernel) against fp32 torch attention on the
-    same q, k, v, to the fp16 bar of the dense parity tests; batch 8 is BASELINE config 5's
-    timed block (T 1024, 12 heads of 64)."""
+    same q, k, v, to the fp16 bar of the dense parity tests; batch 8 is the benchmark's timed
+    GPT-2-small block (T 1024, 12 heads of 64)."""
     require_ext()
     model = gpt_block.build("fused", seed=4)
     attn = model.block.attn
