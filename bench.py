@@ -26,8 +26,8 @@ Printed: ONE JSON line with the contract fields, plus
 * ``configs``: the other benchmark configurations (C128, C64 and C128 causal, the long-context
   shape LONG with its N sweep 512 / 1024 / 4096 / 8192, the GPT-2 attention shape; the fp32
   rung, stage 3, at the reference's CPU-runnable case (B1 H2 N128 D64 fp32) -- timed beside the
-  reference's CPU oracle on that whole
-  workload -- and at C64 and C128 against the fp32 MFMA roof; stage 4 at C64 and C128), each
+  reference's CPU oracle on that whole workload -- and at C64 and C128 against the fp32 MFMA
+  roof; stage 4 at C64 and C128), each
   timed like ``value`` (``ms``: host-issued launches over cache-cold sets, median of three) and
   over 4 cache-resident sets (``warm_ms``), plus one GPU's share of 8-GPU layouts (C64 and LONG
   split over heads, one ring step of LONG split over the sequence);
