@@ -177,8 +177,8 @@ def test_stage5_automatic_tile_on_full_grids(b, h, n, d, dtype, causal, tile, ma
     assert_every_head_close(o0, lse0, q, k, v, causal, d ** -0.5, what=f"tile {tile}")
 
 
-# The D = 64 rule tiles on ragged grids: N = 1056 leaves a partial last query tile (32 of 256 or
-# 128 rows) and a partial last key tile, with and without GQA. The 256-row tile (dense, whole rounds
+# The D = 64 rule tiles on ragged grids: N = 1056 and 4128 leave a partial last query tile (32 of
+# 256 or 128 rows) and a partial last key tile, with and without GQA. The 256-row tile (dense, whole rounds
 # of 256-row workgroups) and the tall 128 x 32 tile (rotated where the K/V per XCD fit 4 MB) are
 # the automatic tiles here; every head is checked against the fp32 reference.
 @pytest.mark.parametrize("b,h,hkv,n,dtype,causal,tile", [
@@ -186,7 +186,10 @@ def test_stage5_automatic_tile_on_full_grids(b, h, n, d, dtype, causal, tile, ma
     (16, 16, 4, 1056, torch.bfloat16, False, (256, 64)),   # GQA, 4 query heads per kv head
     (8, 12, 12, 1056, torch.float16, True, (128, 32)),     # tall, causal, rotated (3.1 MB)
     (8, 12, 4, 1056, torch.bfloat16, False, (128, 32)),    # tall, dense GQA (1.9 rounds of 256)
-], ids=["wide256", "wide256-gqa", "tall-causal", "tall-gqa"])
+    (2, 16, 16, 4128, torch.float16, True, (256, 64)),     # causal 256-row tile, 32-row last tile
+    (2, 16, 4, 4128, torch.bfloat16, True, (256, 64)),     # the same with GQA, bf16
+], ids=["wide256", "wide256-gqa", "tall-causal", "tall-gqa", "wide256-causal",
+        "wide256-causal-gqa"])
 def test_stage5_d64_rule_tiles_on_ragged_grids(b, h, hkv, n, dtype, causal, tile, make_qkv,
                                                reset_overrides):
     require(5, dtype, 64)
