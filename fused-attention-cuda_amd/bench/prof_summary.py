@@ -118,7 +118,10 @@ def collect(outdir: str) -> dict:
     wgs = grid_threads // wg
     waves = grid_threads // 64
     waves_per_wg = max(1, wg // 64)
-    vgpr = int(r0["VGPR_Count"]) + int(r0["Accum_VGPR_Count"])
+    # rocprofv3 reports gfx950's register counts as 4 x ceil(v / 8) for a kernel the compiler
+    # gives v VGPRs (its kernel-resource-usage report: 196 -> 100, 238 -> 120, 150 -> 76), while
+    # the hardware allocates them in granules of 8: the allocation is twice the reported count.
+    vgpr = 2 * (int(r0["VGPR_Count"]) + int(r0["Accum_VGPR_Count"]))
     lds = int(r0["LDS_Block_Size"])
     occ_vgpr = min(MAX_WAVES_PER_SIMD, VGPRS_PER_LANE // max(vgpr, 1))
     wg_lds = LDS_PER_CU // lds if lds else 10**9

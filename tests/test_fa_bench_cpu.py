@@ -121,7 +121,9 @@ def test_prof_summary_derives_its_quantities_from_known_inputs(tmp_path):
     assert t["kernel mean duration"][0].startswith("20.00 us over 2 dispatches")
     assert t["achieved"][0].startswith("859.0 TFLOP/s = 34.4 %")
     assert t["grid"][0].startswith("256 workgroups x 8 waves")
-    assert t["occupancy allowed"][0] == "2 waves/SIMD (VGPR 4, LDS 4, grid 2)"
+    # 104 VGPRs as rocprofv3 reports them are 208 allocated: two waves per SIMD.
+    assert t["registers / LDS"][0].startswith("208 VGPR")
+    assert t["occupancy allowed"][0] == "2 waves/SIMD (VGPR 2, LDS 4, grid 2)"
     assert t["MFMA / VALU per wave"][0] == "256 / 2000 (7.81 VALU per MFMA)"
     assert t["VALU co-issued with MFMA"][0].startswith("25.0 %")
     assert t["resident waves per busy SIMD"][0] == "2.00"
